@@ -1,0 +1,168 @@
+/*
+ * webyiq_q4q8.h -- C ABI of the MI355X (gfx950) int4 x int8 linear-layer path.
+ *
+ * Drop-in for the operator layer of webyIQ's Rust engine
+ * (crates/engine/src/graph.rs:149-222 Builder::{gemv, gemm, matmul, quant},
+ * graph.rs:476-486 head_ops) and the WGSL kernels it specialises
+ * (crates/engine/src/shaders/{quant, gemv_q4q8, gemm_q4q8, argmax}.wgsl).
+ * Only plain pointers and sizes cross the boundary: every pointer argument is
+ * device memory (hipMalloc) owned by the caller; `stream` is a hipStream_t
+ * (NULL = the default stream).  All calls are asynchronous and stream
+ * ordered; no call synchronises the host or allocates memory.
+ *
+ * Tensor layout (webyIQ tools/convert.py:8-12, manifest quant.group = G):
+ *   wq  u32 [N, K/8]   8 int4 codes per word; byte b of word i =
+ *                      q[8i+b] | q[8i+4+b] << 4
+ *   ws  u32 [N, K/G]   low 16 bits f16 scale s, high 16 bits f16 min m;
+ *                      weight = q * s + m  (a zero point z is m = -z * s)
+ *   xq  i8  [M, K]     int8 activations, x ~= xq * dx
+ *   dx  f32 [M, K/GA]  activation scale; GA = K (per token) or 32 (per group,
+ *                      as the reference ships, quant.wgsl:3)
+ *   xs  i32 [M, K/Ge]  sum of xq over each accumulation group, Ge = min(G, GA)
+ *   y   f32 [M, N]
+ *
+ * Output modes (gemv_q4q8.wgsl:4, gemm_q4q8.wgsl:3):
+ *   WQ_MODE_STORE      y = W x
+ *   WQ_MODE_ACCUMULATE y += W x            (residual add)
+ *   WQ_MODE_SILU_MUL   y = silu(W[n] x) * W[n+N] x, gate rows 0..N-1 then up
+ *                      rows N..2N-1 of one [2N, K] tensor (convert.py:184,231)
+ *
+ * Errors mirror the engine's Result<_, String>: a negative status code, and
+ * wq_last_error() returns the message (thread-local, valid until the next call
+ * on the same thread).  Arguments are validated on the host before anything
+ * is launched; on error nothing is launched.
+ */
+#ifndef WEBYIQ_Q4Q8_H
+#define WEBYIQ_Q4Q8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WQ_ABI_VERSION 1
+
+/* status codes */
+#define WQ_OK 0
+#define WQ_EINVAL (-1)     /* null pointer, unknown mode/path */
+#define WQ_ESHAPE (-2)     /* shape outside the supported set */
+#define WQ_EALIGN (-3)     /* pointer alignment */
+#define WQ_EHIP (-4)       /* HIP runtime error at launch */
+#define WQ_EWORKSPACE (-5) /* workspace missing or too small */
+
+/* output modes */
+#define WQ_MODE_STORE 0
+#define WQ_MODE_ACCUMULATE 1
+#define WQ_MODE_SILU_MUL 2
+
+/* which dispatch list a product belongs to (graph.rs:127-146 Path) */
+#define WQ_PATH_DECODE 0  /* one token: GEMV */
+#define WQ_PATH_SPEC 1    /* speculative verify, M <= 8 tokens: GEMV */
+#define WQ_PATH_PREFILL 2 /* a prompt chunk: GEMM on int8 MFMA */
+
+/* Message of the last failed call on this thread ("" after success). */
+const char* wq_last_error(void);
+
+/* WQ_ABI_VERSION of the loaded library. */
+int wq_abi_version(void);
+
+/*
+ * Activation quantiser.  Replaces Builder::quant (graph.rs:216-222) and
+ * quant.wgsl:19-62; semantics of tools/reference.py:43-48 (fq_input).
+ *   v = norm_w ? (x * r) * norm_w : x,  r = 1 / sqrt(mean(x^2) + eps)
+ *   per activation group of GA elements: dx = max|v| / 127,
+ *   xq = dx > 0 ? round_half_even(v / dx) : 0  (IEEE division)
+ *   xs[e] = sum of xq over accumulation group e of Ge = min(G, GA) elements
+ * x f32 [M, K], norm_w f32 [K] or NULL.  GA in {32, K}; G in {32, 128} is
+ * the weight group of the linear layer that will consume xq.
+ * Requires K % 128 == 0; x, norm_w 16-byte aligned; xq 4-byte aligned.
+ */
+int wq_quant_act(void* stream, const float* x, const float* norm_w, float eps,
+                 int64_t M, int64_t K, int32_t GA, int32_t G,
+                 int8_t* xq, float* dx, int32_t* xs);
+
+/*
+ * Decode GEMV, 1 <= M <= 8 tokens.  Replaces Builder::gemv (graph.rs:190-198)
+ * and gemv_q4q8.wgsl:36-131.  Requires K % 128 == 0, G in {32, 128},
+ * GA in {32, K}; wq and xq 16-byte aligned.  wq/ws hold 2N rows in
+ * WQ_MODE_SILU_MUL.  Outputs of WQ_MODE_STORE / WQ_MODE_ACCUMULATE are
+ * bit-reproducible: one fp32 fma chain per (token, row) over the groups in
+ * index order.
+ */
+int wq_gemv(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K,
+            int32_t G, const int8_t* xq, const float* dx, const int32_t* xs,
+            int64_t M, int32_t GA, int32_t mode, float* y);
+
+/*
+ * Prefill GEMM, any M >= 1 (tiles of 128 tokens).  Replaces Builder::gemm
+ * (graph.rs:200-205) and gemm_q4q8.wgsl:46-121.  Same arguments and
+ * constraints as wq_gemv; results are bit-identical to wq_gemv's for the same
+ * inputs (same int32 group sums, same fp32 fold order).
+ */
+int wq_gemm(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K,
+            int32_t G, const int8_t* xq, const float* dx, const int32_t* xs,
+            int64_t M, int32_t GA, int32_t mode, float* y);
+
+/*
+ * Builder::matmul (graph.rs:207-214): WQ_PATH_PREFILL -> wq_gemm, otherwise
+ * wq_gemv (WQ_PATH_DECODE requires M == 1, WQ_PATH_SPEC M <= 8).
+ */
+int wq_matmul(void* stream, int32_t path, const uint32_t* wq, const uint32_t* ws,
+              int64_t N, int64_t K, int32_t G, const int8_t* xq, const float* dx,
+              const int32_t* xs, int64_t M, int32_t GA, int32_t mode, float* y);
+
+/*
+ * Greedy argmax over logits f32 [M, V] (argmax.wgsl:14-43): the maximum over
+ * values > -3e38 (NaN never wins), ties to the lowest index, 0 when no value
+ * qualifies; with ids != NULL the winning index i is mapped to ids[i]
+ * (the draft vocabulary, MAPPED in argmax.wgsl:41).  tok_out u32 [M].
+ */
+int wq_argmax(void* stream, const float* logits, int64_t M, int64_t V,
+              const uint32_t* ids, uint32_t* tok_out);
+
+/*
+ * lm_head GEMV with fused greedy argmax, 1 <= M <= 8.  Replaces the
+ * gemv + argmax pair of head_ops (graph.rs:482-484) with one launch.  The
+ * token is bit-identical to wq_gemv(WQ_MODE_STORE) followed by wq_argmax.
+ * logits f32 [M, V] is written when non-NULL.  `workspace` (device, at least
+ * wq_lm_head_workspace_bytes() bytes) carries the cross-workgroup reduction;
+ * it must be zero before the first call (wq_workspace_clear) and every call
+ * leaves it zero again.  Calls sharing one workspace must not overlap.
+ */
+int wq_lm_head_argmax(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t V,
+                      int64_t K, int32_t G, const int8_t* xq, const float* dx,
+                      const int32_t* xs, int64_t M, int32_t GA, const uint32_t* ids,
+                      float* logits, uint32_t* tok_out, void* workspace,
+                      size_t workspace_bytes);
+
+/* Bytes of workspace wq_lm_head_argmax needs (no counterpart in the
+ * reference, whose argmax runs as a separate single-workgroup dispatch). */
+size_t wq_lm_head_workspace_bytes(void);
+
+/* Zero `bytes` of device memory with a fill kernel (safe inside HIP graph
+ * capture, unlike hipMemsetAsync). */
+int wq_workspace_clear(void* stream, void* workspace, size_t bytes);
+
+/*
+ * Test hooks: wq_gemv / wq_gemm that also store the exact int32 group sums
+ * A[t, row, e] = sum over group e of q[row, k] * xq[t, k] that the kernel
+ * folded into y, into acc i32 [M, rows, K/Ge] (rows = N, or 2N in
+ * WQ_MODE_SILU_MUL).  The reference exposes no such dump; its group sums are
+ * internal to gemv_q4q8.wgsl:68 / gemm_q4q8.wgsl:96.
+ */
+int wq_gemv_debug_acc(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N,
+                      int64_t K, int32_t G, const int8_t* xq, const float* dx,
+                      const int32_t* xs, int64_t M, int32_t GA, int32_t mode, float* y,
+                      int32_t* acc);
+int wq_gemm_debug_acc(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N,
+                      int64_t K, int32_t G, const int8_t* xq, const float* dx,
+                      const int32_t* xs, int64_t M, int32_t GA, int32_t mode, float* y,
+                      int32_t* acc);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WEBYIQ_Q4Q8_H */

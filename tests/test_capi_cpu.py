@@ -1,0 +1,95 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry
+point the header declares, and rejects bad arguments on the host (before any
+launch) with the documented status codes and messages -- the analogue of the
+engine's host-side shape checks (graph.rs:368-380, manifest.rs:82-84)."""
+import ctypes
+import re
+
+import pytest
+
+from webyiq_amd import _lib
+
+L = _lib.load()
+A16 = ctypes.c_void_p(0x10000)  # aligned non-null dummies: validation fails before any use
+A4 = ctypes.c_void_p(0x10004)
+
+
+def declared_symbols():
+    text = open(_lib.HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\*?\s+\*?(wq_[a-z_0-9]+)\(", text, re.M)))
+
+
+def test_exports_every_declared_symbol():
+    names = declared_symbols()
+    assert len(names) == 12
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(_lib.PROTOTYPES)
+    assert L.wq_abi_version() == 1
+    assert L.wq_lm_head_workspace_bytes() >= 72
+
+
+def gemv(*, wq=A16, ws=A4, N=64, K=2048, G=128, xq=A16, dx=A4, xs=A4, M=1, GA=None, mode=0, y=A4,
+         fn="wq_gemv"):
+    GA = K if GA is None else GA
+    return getattr(L, fn)(None, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y)
+
+
+def err():
+    return L.wq_last_error().decode()
+
+
+@pytest.mark.parametrize("fn", ["wq_gemv", "wq_gemm"])
+def test_linear_argument_errors(fn):
+    assert gemv(wq=None, fn=fn) == _lib.WQ_EINVAL and "wq is NULL" in err()
+    assert gemv(y=None, fn=fn) == _lib.WQ_EINVAL
+    assert gemv(mode=3, fn=fn) == _lib.WQ_EINVAL and "unknown mode" in err()
+    assert gemv(K=2000, fn=fn) == _lib.WQ_ESHAPE and "multiple of 128" in err()
+    assert gemv(K=64, fn=fn) == _lib.WQ_ESHAPE
+    assert gemv(G=64, fn=fn) == _lib.WQ_ESHAPE and "quant group" in err()
+    assert gemv(GA=64, fn=fn) == _lib.WQ_ESHAPE and "activation group" in err()
+    assert gemv(N=0, fn=fn) == _lib.WQ_ESHAPE
+    assert gemv(M=0, fn=fn) == _lib.WQ_ESHAPE
+    assert gemv(wq=A4, fn=fn) == _lib.WQ_EALIGN and "16-byte" in err()
+    assert gemv(xq=ctypes.c_void_p(0x10008), fn=fn) == _lib.WQ_EALIGN
+    assert gemv(ws=ctypes.c_void_p(0x10002), fn=fn) == _lib.WQ_EALIGN
+
+
+def test_gemv_token_and_k_limits():
+    assert gemv(M=9) == _lib.WQ_ESHAPE and "M = 9" in err()
+    assert gemv(K=2048 * 9) == _lib.WQ_ESHAPE
+    # the GEMM takes any M (and the same K)
+    assert gemv(M=9, mode=7, fn="wq_gemm") == _lib.WQ_EINVAL
+
+
+def test_matmul_paths():
+    args = [A16, A4, 64, 2048, 128, A16, A4, A4, 2, 2048, 0, A4]
+    assert L.wq_matmul(None, 7, *args) == _lib.WQ_EINVAL and "unknown path" in err()
+    assert L.wq_matmul(None, _lib.PATH_DECODE, *args) == _lib.WQ_ESHAPE and "M = 1" in err()
+
+
+def test_quant_errors():
+    q = L.wq_quant_act
+    assert q(None, None, None, 1e-6, 1, 2048, 2048, 128, A16, A4, A4) == _lib.WQ_EINVAL
+    assert q(None, A16, None, 1e-6, 1, 2000, 2000, 128, A16, A4, A4) == _lib.WQ_ESHAPE
+    assert q(None, A16, None, 1e-6, 1, 2048, 64, 128, A16, A4, A4) == _lib.WQ_ESHAPE
+    assert q(None, A4, None, 1e-6, 1, 2048, 2048, 128, A16, A4, A4) == _lib.WQ_EALIGN
+    assert q(None, A16, A16, -1.0, 1, 2048, 2048, 128, A16, A4, A4) == _lib.WQ_EINVAL
+
+
+def test_argmax_and_lm_head_errors():
+    assert L.wq_argmax(None, None, 1, 10, None, A4) == _lib.WQ_EINVAL
+    assert L.wq_argmax(None, A4, 1, 0, None, A4) == _lib.WQ_ESHAPE
+    lm = L.wq_lm_head_argmax
+    base = [None, A16, A4, 1000, 2048, 128, A16, A4, A4, 1, 2048, None, None, A4]
+    assert lm(*base, None, 128) == _lib.WQ_EWORKSPACE and "workspace" in err()
+    assert lm(*base, A16, 8) == _lib.WQ_EWORKSPACE
+    base[-1] = None
+    assert lm(*base, A16, 128) == _lib.WQ_EINVAL and "tok_out" in err()
+    assert L.wq_workspace_clear(None, None, 16) == _lib.WQ_EINVAL
+
+
+def test_python_wrapper_raises_wq_error():
+    with pytest.raises(_lib.WqError) as e:
+        _lib.call("wq_gemv", None, None, A4, 64, 2048, 128, A16, A4, A4, 1, 2048, 0, A4)
+    assert e.value.code == _lib.WQ_EINVAL and "wq is NULL" in e.value.message

@@ -1,0 +1,262 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the CPU oracle
+on the same seeded inputs.
+
+Bars (stated per test):
+  * int8 codes, dx, xs, int32 group sums, argmax tokens: bit-exact;
+  * fp32 outputs of modes 0/1: bit-exact against the oracle's canonical fold
+    (one fma chain per output over the groups in order);
+  * mode 2 (SiLU): within 1e-5 of the oracle (device expf vs libm expf);
+  * every fp32 output within rel 1e-3 (max-norm) of the torch fake-quant path.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from oracle import reference as ref
+from webyiq_amd import ops
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def note(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def dev_acts(xq, dx, xs, GA, G):
+    return ops.Acts(dev(xq), dev(dx), dev(xs), GA, G)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def setup_linear(seed, M, K, rows, G, GA):
+    rng = np.random.default_rng(seed)
+    wq, ws = ref.make_weight(rng, rows, K, G)
+    x = ref.make_activations(rng, M, K)
+    xq, dx, xs = orc.quant_act(x, GA, G)
+    return wq, ws, x, xq, dx, xs
+
+
+# ------------------------------------------------------------- quantiser ----
+
+@pytest.mark.parametrize("M,K,GA,G,norm", [
+    (1, 2048, None, 128, False), (3, 6144, None, 128, False), (8, 2048, None, 32, False),
+    (5, 1024, 32, 128, False), (2, 128, None, 128, False), (64, 2048, None, 128, False),
+    (4, 2048, None, 128, True), (3, 6144, 32, 32, True),
+])
+def test_quant_act_bit_exact(M, K, GA, G, norm):
+    note(f"quant M={M} K={K} GA={GA} G={G} norm={norm}")
+    rng = np.random.default_rng(M * 7 + K)
+    x = ref.make_activations(rng, M, K)
+    x[M - 1, : K // 2] = 0.0 if M > 1 else x[M - 1, : K // 2]
+    nw = rng.normal(1.0, 0.2, size=K).astype(np.float32) if norm else None
+    xq, dx, xs = orc.quant_act(x, GA, G, norm_w=nw, eps=1e-6)
+    a = ops.quant(dev(x), norm=None if nw is None else dev(nw), eps=1e-6, GA=GA, G=G)
+    assert np.array_equal(host(a.xq), xq)
+    assert np.array_equal(host(a.dx).view(np.uint32), dx.view(np.uint32))
+    assert np.array_equal(host(a.xs), xs)
+
+
+def test_quant_zero_rows_and_ties():
+    note("quant zero rows / ties")
+    x = np.zeros((3, 256), np.float32)
+    x[0, :6] = [127.0, 2.5, 3.5, -2.5, 0.5, -126.5]
+    x[2] = np.linspace(-3, 3, 256, dtype=np.float32)
+    for GA in (None, 32):
+        xq, dx, xs = orc.quant_act(x, GA, 128)
+        a = ops.quant(dev(x), GA=GA, G=128)
+        assert np.array_equal(host(a.xq), xq)
+        assert np.array_equal(host(a.dx), dx)
+        assert np.array_equal(host(a.xs), xs)
+
+
+# ------------------------------------------------------------------ GEMV ----
+
+GEMV_CASES = [
+    # M, K, N, G, GA(None = per token), mode
+    (1, 2048, 6144, 128, None, 0),   # BASELINE cfg 1 shape
+    (1, 2048, 2048, 128, None, 1),
+    (1, 6144, 2048, 128, None, 1),   # cfg 2 down
+    (1, 2048, 6144, 128, None, 2),   # cfg 2 gate_up (2 x 6144 rows)
+    (2, 2048, 512, 128, None, 0),    # cfg 3 k/v
+    (3, 2048, 1000, 128, None, 0),   # ragged N, M rounded up to 4
+    (4, 6144, 2048, 128, None, 0),
+    (8, 2048, 6144, 128, None, 2),
+    (8, 6144, 2048, 128, None, 1),
+    (1, 128, 77, 128, None, 0),      # one group, partial pass
+    (5, 1024, 300, 32, None, 0),
+    (2, 2048, 256, 32, 32, 1),       # reference-native: G = 32, GA = 32
+    (3, 4096, 130, 128, 32, 2),
+    (7, 3072, 96, 32, None, 0),      # K not a multiple of 2048
+]
+
+
+@pytest.mark.parametrize("M,K,N,G,GA,mode", GEMV_CASES)
+def test_gemv_bit_exact(M, K, N, G, GA, mode):
+    note(f"gemv M={M} K={K} N={N} G={G} GA={GA} mode={mode}")
+    rows = 2 * N if mode == 2 else N
+    wq, ws, x, xq, dx, xs = setup_linear(M * 1000 + N, M, K, rows, G, GA)
+    gaa = K if GA is None else GA
+    y0 = np.random.default_rng(1).normal(size=(M, N)).astype(np.float32) if mode == 1 else None
+    want = orc.linear(wq, ws, K, G, xq, dx, xs, mode=mode, y=y0, GA=gaa)
+    acc_want = orc.group_acc(wq, K, min(G, gaa), xq)
+
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
+    a = dev_acts(xq, dx, xs, gaa, G)
+    y = dev(y0) if mode == 1 else None
+    y, acc = ops.group_sums(ops.PATH_SPEC, w, a, mode=mode, y=y)
+    assert np.array_equal(host(acc), acc_want)
+    got = host(y)
+    if mode == 2:
+        assert rel_err(got, want) < 1e-5
+    else:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the plain entry point computes the same values
+    y2 = ops.gemv(w, a, mode=mode, y=dev(y0) if mode == 1 else None)
+    assert np.array_equal(host(y2), got)
+    # and the torch fake-quant reference agrees within the stated tolerance
+    fq = ref.FakeQuantLinear(wq, ws, K, G, mode=mode, GA=GA)(x, y0).numpy()
+    assert rel_err(got, fq) < 1e-3
+
+
+# ------------------------------------------------------------------ GEMM ----
+
+GEMM_CASES = [
+    (256, 2048, 512, 128, None, 0),
+    (100, 2048, 384, 128, None, 1),   # ragged M tile
+    (130, 6144, 256, 128, None, 0),
+    (64, 2048, 192, 128, None, 2),
+    (33, 1024, 100, 128, None, 0),    # ragged N tile
+    (96, 2048, 256, 32, 32, 0),       # reference-native groups
+    (17, 512, 64, 32, None, 1),
+    (48, 1024, 128, 128, 32, 2),
+    (1, 128, 16, 128, None, 0),
+]
+
+
+@pytest.mark.parametrize("M,K,N,G,GA,mode", GEMM_CASES)
+def test_gemm_bit_exact(M, K, N, G, GA, mode):
+    note(f"gemm M={M} K={K} N={N} G={G} GA={GA} mode={mode}")
+    rows = 2 * N if mode == 2 else N
+    wq, ws, x, xq, dx, xs = setup_linear(M * 31 + N, M, K, rows, G, GA)
+    gaa = K if GA is None else GA
+    y0 = np.random.default_rng(2).normal(size=(M, N)).astype(np.float32) if mode == 1 else None
+    want = orc.linear(wq, ws, K, G, xq, dx, xs, mode=mode, y=y0, GA=gaa)
+    acc_want = orc.group_acc(wq, K, min(G, gaa), xq)
+
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
+    a = dev_acts(xq, dx, xs, gaa, G)
+    y, acc = ops.group_sums(ops.PATH_PREFILL, w, a, mode=mode, y=dev(y0) if mode == 1 else None)
+    assert np.array_equal(host(acc), acc_want)
+    got = host(y)
+    if mode == 2:
+        assert rel_err(got, want) < 1e-5
+    else:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    fq = ref.FakeQuantLinear(wq, ws, K, G, mode=mode, GA=GA)(x, y0).numpy()
+    assert rel_err(got, fq) < 1e-3
+
+
+def test_gemm_matches_gemv_rows():
+    """Decode vs prefill cross-check (the reference's --ppl / --sequential
+    harnesses, crates/cli/src/main.rs:209-250): each GEMM row equals the GEMV
+    of that token, bit for bit."""
+    note("gemm vs gemv rows")
+    M, K, N = 40, 2048, 1024
+    wq, ws, x, xq, dx, xs = setup_linear(5, M, K, N, 128, None)
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, 128)
+    a = dev_acts(xq, dx, xs, K, 128)
+    yg = host(ops.matmul(ops.PATH_PREFILL, w, a))
+    for t0 in range(0, M, 8):
+        sub = dev_acts(xq[t0:t0 + 8], dx[t0:t0 + 8], xs[t0:t0 + 8], K, 128)
+        yv = host(ops.matmul(ops.PATH_SPEC, w, sub))
+        assert np.array_equal(yv, yg[t0:t0 + 8])
+
+
+# -------------------------------------------------------------- argmax ------
+
+def test_argmax_standalone():
+    note("argmax standalone")
+    rng = np.random.default_rng(3)
+    v = rng.normal(size=(4, 151936)).astype(np.float32)
+    v[1, [5, 77777, 150000]] = 50.0
+    v[2, 9] = np.nan
+    v[3, :] = -np.inf
+    ids = np.arange(151936, dtype=np.uint32)[::-1].copy()
+    got = host(ops.argmax(dev(v))).astype(np.uint32)
+    assert np.array_equal(got, orc.argmax(v))
+    got = host(ops.argmax(dev(v), ids=dev(ids.view(np.int32)))).astype(np.uint32)
+    assert np.array_equal(got, orc.argmax(v, ids))
+
+
+@pytest.mark.parametrize("M,V,G,mapped", [(1, 32768, 128, False), (8, 32768, 128, True),
+                                          (3, 5000, 32, False), (1, 151936, 128, False)])
+def test_lm_head_argmax(M, V, G, mapped):
+    note(f"lm_head M={M} V={V} G={G} mapped={mapped}")
+    K = 2048
+    wq, ws, x, xq, dx, xs = setup_linear(V + M, M, K, V, G, None)
+    # plant exact ties: duplicate the winner's row at a lower and a higher index
+    logits = orc.linear(wq, ws, K, G, xq, dx, xs)
+    win = int(orc.argmax(logits)[0])
+    lo, hi = max(0, win // 2 - 1), min(V - 1, win + 3)
+    wq[lo], ws[lo] = wq[win], ws[win]
+    wq[hi], ws[hi] = wq[win], ws[win]
+    logits = orc.linear(wq, ws, K, G, xq, dx, xs)
+    ids = np.sort(np.random.default_rng(4).choice(151936, V, replace=False)).astype(np.uint32) if mapped else None
+    want = orc.argmax(logits, ids)
+    assert want[0] == (ids[lo] if mapped else lo)
+
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
+    a = dev_acts(xq, dx, xs, K, G)
+    lg = torch.empty((M, V), dtype=torch.float32, device=DEV)
+    ws_dev = ops.lm_head_workspace()
+    d_ids = dev(ids.view(np.int32)) if mapped else None
+    tok = ops.lm_head_argmax(w, a, ids=d_ids, logits=lg, workspace=ws_dev)
+    assert np.array_equal(host(tok).astype(np.uint32), want)
+    assert np.array_equal(host(lg).view(np.uint32), logits.view(np.uint32))
+    # second call on the same workspace (it must have been left zeroed), no logits
+    tok2 = ops.lm_head_argmax(w, a, ids=d_ids, workspace=ws_dev)
+    assert np.array_equal(host(tok2).astype(np.uint32), want)
+    assert np.all(host(ws_dev) == 0)
+
+
+# ------------------------------------------------------- MLP block (cfg 2) --
+
+def test_decode_mlp_block():
+    """gate_up (mode 2) -> per-token re-quant -> down (mode 1), graph.rs:318-328."""
+    note("mlp block")
+    hd, ffn = 2048, 6144
+    rng = np.random.default_rng(11)
+    wgu, sgu = ref.make_weight(rng, 2 * ffn, hd, 128)
+    wd, sd = ref.make_weight(rng, hd, ffn, 128)
+    x = ref.make_activations(rng, 1, hd)
+    resid = rng.normal(size=(1, hd)).astype(np.float32)
+
+    xq, dx, xs = orc.quant_act(x, None, 128)
+    h_want = orc.linear(wgu, sgu, hd, 128, xq, dx, xs, mode=2)
+
+    a = ops.quant(dev(x), G=128)
+    h = ops.gemv(ops.Q4Tensor.from_numpy(wgu, sgu, hd, 128), a, mode=2)
+    h_got = host(h)
+    assert rel_err(h_got, h_want) < 1e-5
+    # re-quant of the device h is bit-exact against the oracle on the same h
+    a2 = ops.quant(h, G=128)
+    hq, hdx, hxs = orc.quant_act(h_got, None, 128)
+    assert np.array_equal(host(a2.xq), hq)
+    y = dev(resid)
+    ops.gemv(ops.Q4Tensor.from_numpy(wd, sd, ffn, 128), a2, mode=1, y=y)
+    want = orc.linear(wd, sd, ffn, 128, hq, hdx, hxs, mode=1, y=resid)
+    assert np.array_equal(host(y).view(np.uint32), want.view(np.uint32))
+    # torch fake-quant chain
+    gu = ref.FakeQuantLinear(wgu, sgu, hd, 128, mode=2)(x)
+    out = ref.FakeQuantLinear(wd, sd, ffn, 128, mode=1)(gu, resid).numpy()
+    assert rel_err(host(y), out) < 1e-3

@@ -1,0 +1,64 @@
+"""Build libwebyiq_q4q8.so (gfx950) in-tree with hipcc.
+
+  python -m webyiq_amd.build          # compile every kernel + the C ABI
+
+Each .hip translation unit is compiled in parallel into webyiq_amd/_build/,
+then linked into webyiq_amd/libwebyiq_q4q8.so next to this file.  Flags:
+  --offload-arch=gfx950 only (no other targets, no CUDA/HIP dual paths);
+  -Xclang -target-feature -Xclang -packed-fp32-ops: no packed fp32 ops;
+  no fast-math: divisions and the fp32 epilogues keep IEEE semantics that
+  the CPU oracle reproduces bit for bit.
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+BUILD = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "libwebyiq_q4q8.so")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+SOURCES = ["capi.hip", "quant_act.hip", "gemv_q4q8.hip", "gemm_q4q8.hip", "argmax.hip"]
+CFLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def build(verbose=False):
+    os.makedirs(BUILD, exist_ok=True)
+    procs = []
+    objs = []
+    for src in SOURCES:
+        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+        objs.append(obj)
+        cmd = [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
+    failed = []
+    for src, p in procs:
+        out, _ = p.communicate()
+        text = "\n".join(l for l in out.decode(errors="replace").splitlines()
+                         if "packed-fp32-ops" not in l)
+        if p.returncode != 0:
+            failed.append((src, text))
+        elif verbose and text.strip():
+            print(text)
+    if failed:
+        for src, text in failed:
+            print(f"--- {src} failed ---\n{text}", file=sys.stderr)
+        raise RuntimeError("hipcc failed for " + ", ".join(s for s, _ in failed))
+    tmp = LIB + ".tmp"
+    subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp], check=True)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,266 @@
+// C ABI of the int4 x int8 path (include/webyiq_q4q8.h).
+//
+// Every entry point validates its arguments on the host first and returns a
+// status code with a thread-local message, like the engine's
+// Result<_, String> (webyIQ crates/engine/src/graph.rs:186-222,368-380,
+// manifest.rs:82-84).  Nothing is launched when validation fails, so all
+// error paths are exercisable without a GPU.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/webyiq_q4q8.h"
+#include "launch.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int ok() {
+    g_err.clear();
+    return WQ_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(WQ_EHIP, "%s: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+#define REQUIRE_PTR(p)                                                   \
+    do {                                                                 \
+        if (!(p)) return fail(WQ_EINVAL, "%s: %s is NULL", fn, #p);      \
+    } while (0)
+#define REQUIRE_ALIGN(p, a)                                                              \
+    do {                                                                                 \
+        if (!aligned((p), (a))) return fail(WQ_EALIGN, "%s: %s not %d-byte aligned", fn, \
+                                            #p, (int)(a));                               \
+    } while (0)
+
+// Group / granularity rules shared by the quantiser and the products
+// (graph.rs:378 requires K % 128; manifest.rs:82 fixed G = 32, G = 128 added).
+int check_groups(const char* fn, int64_t K, int32_t G, int32_t GA) {
+    if (K < 128 || K % 128 != 0)
+        return fail(WQ_ESHAPE, "%s: K = %lld must be a positive multiple of 128", fn, (long long)K);
+    if (G != 32 && G != 128)
+        return fail(WQ_ESHAPE, "%s: unsupported quant group G = %d (32 or 128)", fn, G);
+    if (GA != 32 && (int64_t)GA != K)
+        return fail(WQ_ESHAPE, "%s: activation group GA = %d must be 32 or K = %lld", fn, GA,
+                    (long long)K);
+    return WQ_OK;
+}
+
+int check_linear(const char* fn, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K,
+                 int32_t G, const int8_t* xq, const float* dx, const int32_t* xs, int64_t M,
+                 int32_t GA, int32_t mode, const float* y, bool need_y) {
+    REQUIRE_PTR(wq);
+    REQUIRE_PTR(ws);
+    REQUIRE_PTR(xq);
+    REQUIRE_PTR(dx);
+    REQUIRE_PTR(xs);
+    if (need_y) REQUIRE_PTR(y);
+    if (mode < WQ_MODE_STORE || mode > WQ_MODE_SILU_MUL)
+        return fail(WQ_EINVAL, "%s: unknown mode %d", fn, mode);
+    if (N < 1 || N > (int64_t(1) << 30))
+        return fail(WQ_ESHAPE, "%s: N = %lld out of range", fn, (long long)N);
+    if (M < 1 || M > (int64_t(1) << 30))
+        return fail(WQ_ESHAPE, "%s: M = %lld out of range", fn, (long long)M);
+    int rc = check_groups(fn, K, G, GA);
+    if (rc) return rc;
+    REQUIRE_ALIGN(wq, 16);
+    REQUIRE_ALIGN(xq, 16);
+    REQUIRE_ALIGN(ws, 4);
+    REQUIRE_ALIGN(dx, 4);
+    REQUIRE_ALIGN(xs, 4);
+    if (y) REQUIRE_ALIGN(y, 4);
+    return WQ_OK;
+}
+
+// The decode GEMV keeps <= 8 tokens in registers and <= 8 passes of 2048
+// codes per row (one workgroup of <= 16 waves).
+int check_gemv_shape(const char* fn, int64_t M, int64_t K) {
+    if (M > wq::kGemvMaxTokens)
+        return fail(WQ_ESHAPE, "%s: M = %lld tokens exceeds the decode GEMV limit of %d", fn,
+                    (long long)M, wq::kGemvMaxTokens);
+    if (K > 8 * wq::kGemvPassK)
+        return fail(WQ_ESHAPE, "%s: K = %lld exceeds the decode GEMV limit of %d", fn,
+                    (long long)K, 8 * wq::kGemvPassK);
+    return WQ_OK;
+}
+
+wq::LinearArgs make_args(const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K, int32_t G,
+                         const int8_t* xq, const float* dx, const int32_t* xs, int64_t M,
+                         int32_t GA, int32_t mode, float* y, int32_t* acc) {
+    wq::LinearArgs a{};
+    a.wq = wq;
+    a.ws = ws;
+    a.N = N;
+    a.K = K;
+    a.G = G;
+    a.xq = xq;
+    a.dx = dx;
+    a.xs = xs;
+    a.M = M;
+    a.GA = GA;
+    a.mode = mode;
+    a.y = y;
+    a.acc_dump = acc;
+    return a;
+}
+
+int gemv_impl(const char* fn, void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N,
+              int64_t K, int32_t G, const int8_t* xq, const float* dx, const int32_t* xs,
+              int64_t M, int32_t GA, int32_t mode, float* y, int32_t* acc) {
+    int rc = check_linear(fn, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, true);
+    if (rc) return rc;
+    rc = check_gemv_shape(fn, M, K);
+    if (rc) return rc;
+    auto a = make_args(wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, acc);
+    return hip_status(wq::launch_gemv(a, static_cast<hipStream_t>(stream)), fn);
+}
+
+int gemm_impl(const char* fn, void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N,
+              int64_t K, int32_t G, const int8_t* xq, const float* dx, const int32_t* xs,
+              int64_t M, int32_t GA, int32_t mode, float* y, int32_t* acc) {
+    int rc = check_linear(fn, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, true);
+    if (rc) return rc;
+    auto a = make_args(wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, acc);
+    return hip_status(wq::launch_gemm(a, static_cast<hipStream_t>(stream)), fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* wq_last_error(void) { return g_err.c_str(); }
+
+int wq_abi_version(void) { return WQ_ABI_VERSION; }
+
+int wq_quant_act(void* stream, const float* x, const float* norm_w, float eps, int64_t M,
+                 int64_t K, int32_t GA, int32_t G, int8_t* xq, float* dx, int32_t* xs) {
+    const char* fn = "wq_quant_act";
+    REQUIRE_PTR(x);
+    REQUIRE_PTR(xq);
+    REQUIRE_PTR(dx);
+    REQUIRE_PTR(xs);
+    if (M < 1 || M > (int64_t(1) << 30))
+        return fail(WQ_ESHAPE, "%s: M = %lld out of range", fn, (long long)M);
+    int rc = check_groups(fn, K, G, GA);
+    if (rc) return rc;
+    if (K > (int64_t(1) << 24)) return fail(WQ_ESHAPE, "%s: K = %lld too large", fn, (long long)K);
+    REQUIRE_ALIGN(x, 16);
+    if (norm_w) REQUIRE_ALIGN(norm_w, 16);
+    REQUIRE_ALIGN(xq, 4);
+    REQUIRE_ALIGN(dx, 4);
+    REQUIRE_ALIGN(xs, 4);
+    if (norm_w && !(eps >= 0.0f)) return fail(WQ_EINVAL, "%s: eps must be >= 0", fn);
+    wq::QuantArgs a{x, norm_w, eps, M, K, GA, G, xq, dx, xs};
+    return hip_status(wq::launch_quant_act(a, static_cast<hipStream_t>(stream)), fn);
+}
+
+int wq_gemv(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K, int32_t G,
+            const int8_t* xq, const float* dx, const int32_t* xs, int64_t M, int32_t GA,
+            int32_t mode, float* y) {
+    return gemv_impl("wq_gemv", stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, nullptr);
+}
+
+int wq_gemm(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K, int32_t G,
+            const int8_t* xq, const float* dx, const int32_t* xs, int64_t M, int32_t GA,
+            int32_t mode, float* y) {
+    return gemm_impl("wq_gemm", stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, nullptr);
+}
+
+int wq_gemv_debug_acc(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K,
+                      int32_t G, const int8_t* xq, const float* dx, const int32_t* xs, int64_t M,
+                      int32_t GA, int32_t mode, float* y, int32_t* acc) {
+    const char* fn = "wq_gemv_debug_acc";
+    REQUIRE_PTR(acc);
+    return gemv_impl(fn, stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, acc);
+}
+
+int wq_gemm_debug_acc(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K,
+                      int32_t G, const int8_t* xq, const float* dx, const int32_t* xs, int64_t M,
+                      int32_t GA, int32_t mode, float* y, int32_t* acc) {
+    const char* fn = "wq_gemm_debug_acc";
+    REQUIRE_PTR(acc);
+    return gemm_impl(fn, stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, acc);
+}
+
+int wq_matmul(void* stream, int32_t path, const uint32_t* wq, const uint32_t* ws, int64_t N,
+              int64_t K, int32_t G, const int8_t* xq, const float* dx, const int32_t* xs,
+              int64_t M, int32_t GA, int32_t mode, float* y) {
+    const char* fn = "wq_matmul";
+    switch (path) {
+        case WQ_PATH_PREFILL:
+            return gemm_impl(fn, stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, nullptr);
+        case WQ_PATH_DECODE:
+            if (M != 1) return fail(WQ_ESHAPE, "%s: decode path takes M = 1, got %lld", fn, (long long)M);
+            return gemv_impl(fn, stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, nullptr);
+        case WQ_PATH_SPEC:
+            return gemv_impl(fn, stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, nullptr);
+        default:
+            return fail(WQ_EINVAL, "%s: unknown path %d", fn, path);
+    }
+}
+
+int wq_argmax(void* stream, const float* logits, int64_t M, int64_t V, const uint32_t* ids,
+              uint32_t* tok_out) {
+    const char* fn = "wq_argmax";
+    REQUIRE_PTR(logits);
+    REQUIRE_PTR(tok_out);
+    if (M < 1 || M > (int64_t(1) << 30))
+        return fail(WQ_ESHAPE, "%s: M = %lld out of range", fn, (long long)M);
+    if (V < 1 || V > (int64_t)0xFFFFFFFEll)
+        return fail(WQ_ESHAPE, "%s: V = %lld out of range", fn, (long long)V);
+    REQUIRE_ALIGN(logits, 4);
+    REQUIRE_ALIGN(tok_out, 4);
+    return hip_status(wq::launch_argmax(logits, M, V, ids, tok_out, static_cast<hipStream_t>(stream)), fn);
+}
+
+size_t wq_lm_head_workspace_bytes(void) { return wq::kArgmaxWorkspaceBytes; }
+
+int wq_workspace_clear(void* stream, void* workspace, size_t bytes) {
+    const char* fn = "wq_workspace_clear";
+    REQUIRE_PTR(workspace);
+    if (bytes == 0) return ok();
+    return hip_status(wq::launch_fill_zero(workspace, bytes, static_cast<hipStream_t>(stream)), fn);
+}
+
+int wq_lm_head_argmax(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t V, int64_t K,
+                      int32_t G, const int8_t* xq, const float* dx, const int32_t* xs, int64_t M,
+                      int32_t GA, const uint32_t* ids, float* logits, uint32_t* tok_out,
+                      void* workspace, size_t workspace_bytes) {
+    const char* fn = "wq_lm_head_argmax";
+    int rc = check_linear(fn, wq, ws, V, K, G, xq, dx, xs, M, GA, WQ_MODE_STORE, logits, false);
+    if (rc) return rc;
+    rc = check_gemv_shape(fn, M, K);
+    if (rc) return rc;
+    REQUIRE_PTR(tok_out);
+    REQUIRE_ALIGN(tok_out, 4);
+    if (V > (int64_t)0xFFFFFFFEll) return fail(WQ_ESHAPE, "%s: V = %lld out of range", fn, (long long)V);
+    if (!workspace || workspace_bytes < wq::kArgmaxWorkspaceBytes)
+        return fail(WQ_EWORKSPACE, "%s: workspace of %zu bytes required", fn,
+                    (size_t)wq::kArgmaxWorkspaceBytes);
+    REQUIRE_ALIGN(workspace, 8);
+    auto a = make_args(wq, ws, V, K, G, xq, dx, xs, M, GA, WQ_MODE_STORE, logits, nullptr);
+    wq::ArgmaxArgs am{};
+    am.ids = ids;
+    am.tok_out = tok_out;
+    am.keys = static_cast<unsigned long long*>(workspace);
+    am.ticket = reinterpret_cast<unsigned int*>(static_cast<unsigned char*>(workspace) + 64);
+    return hip_status(wq::launch_lm_head_argmax(a, am, static_cast<hipStream_t>(stream)), fn);
+}
+
+}  // extern "C"

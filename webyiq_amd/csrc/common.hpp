@@ -1,0 +1,85 @@
+// Shared device helpers for the gfx950 int4 x int8 kernels.
+//
+// Data layout (webyIQ's packed-int4 format, tools/convert.py:8-12):
+//   wq  u32 [N, K/8]   word i of row n holds codes 8i..8i+7:
+//                      byte b = q[8i+b] | q[8i+4+b] << 4, so
+//                      w & 0x0F0F0F0F        -> int8 codes 8i+0..3
+//                      (w >> 4) & 0x0F0F0F0F -> int8 codes 8i+4..7
+//   ws  u32 [N, K/G]   low half f16 scale s, high half f16 min m; w = q*s + m
+//   xq  i8  [M, K]     activations, x ~= xq * dx
+//   dx  f32 [M, K/GA]  GA = K (per token) or 32
+//   xs  i32 [M, K/Ge]  sum of xq per accumulation group, Ge = min(G, GA)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wq {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kNibbleMask = 0x0F0F0F0Fu;
+
+__device__ __forceinline__ float f16lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xFFFFu));
+}
+__device__ __forceinline__ float f16hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(w >> 16));
+}
+
+// Signed 4 x int8 dot product with int32 accumulate (v_dot4_i32_i8); the
+// reference's dot4I8Packed (crates/engine/src/gpu.rs:70-75 defines it as the
+// sign-extended byte dot).  Nibble codes 0..15 are non-negative int8.
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// 32 codes (one 16-byte load of a packed row) against 32 int8 activations.
+__device__ __forceinline__ int dot32(const uint4& w, const uint4& xa, const uint4& xb) {
+    int acc = 0;
+    acc = dot4(w.x & kNibbleMask, xa.x, acc);
+    acc = dot4((w.x >> 4) & kNibbleMask, xa.y, acc);
+    acc = dot4(w.y & kNibbleMask, xa.z, acc);
+    acc = dot4((w.y >> 4) & kNibbleMask, xa.w, acc);
+    acc = dot4(w.z & kNibbleMask, xb.x, acc);
+    acc = dot4((w.z >> 4) & kNibbleMask, xb.y, acc);
+    acc = dot4(w.w & kNibbleMask, xb.z, acc);
+    acc = dot4((w.w >> 4) & kNibbleMask, xb.w, acc);
+    return acc;
+}
+
+// Sum over the 4 lanes of a quad (exact int32, order-free) via DPP.
+__device__ __forceinline__ int quad_sum(int v) {
+    v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);  // quad_perm [1,0,3,2]
+    v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);  // quad_perm [2,3,0,1]
+    return v;
+}
+
+// Non-temporal 16-byte load for weights that are streamed exactly once.
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+    v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+    return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+
+__device__ __forceinline__ uint4 load16(const void* p) {
+    return *reinterpret_cast<const uint4*>(p);
+}
+
+// SiLU(a) * u in the reference's form a / (1 + exp(-a)) * u
+// (crates/engine/src/shaders/gemv_q4q8.wgsl:128).
+__device__ __forceinline__ float silu_mul(float a, float u) {
+    return a / (1.0f + expf(-a)) * u;
+}
+
+// Order-preserving key for argmax over floats: larger value -> larger key,
+// equal values -> the lower index wins (its complement is larger).  -0.0 is
+// folded onto +0.0 so that the two compare equal, as `>` does.
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
+    uint32_t u = __float_as_uint(v + 0.0f);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
+}
+
+}  // namespace wq

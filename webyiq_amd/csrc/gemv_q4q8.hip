@@ -1,0 +1,327 @@
+// Decode GEMV, M <= 8 tokens (webyIQ crates/engine/src/shaders/gemv_q4q8.wgsl,
+// host side Builder::gemv in crates/engine/src/graph.rs:190-198), and the
+// lm_head GEMV with fused greedy argmax (graph.rs:476-486 + argmax.wgsl).
+//
+// y[t,n] = sum_g dx * (s[n,g] * A[t,n,g] + m[n,g] * X[t,g]),
+// A = sum over group g of q * xq (int32, exact), X = sum of xq over g.
+//
+// MI355X mapping.  The packed weight matrix is one HBM stream.  A wavefront
+// pass reads 1 KiB of one row (64 lanes x 16 B: one fully coalesced
+// global_load_dwordx4), i.e. 2048 codes; a row of K codes takes J = K/2048
+// passes.  Wave w of a workgroup serves pass j = w % J for rows
+// slot, slot + nslots, ... (slot = w / J), so each lane keeps the 32
+// activations of its pass in registers for every token.  All weight loads of
+// a workgroup are issued before the first one is consumed (IPW rows per wave),
+// so the whole matrix is in flight at once across the chip.
+//
+// Each lane computes its 32-code dot product with 8 v_dot4_i32_i8, a quad of
+// lanes (DPP) completes a 128-group; the exact int32 group sums go to LDS.
+// The fp32 epilogue then runs one fma chain per (token, row) over the groups
+// in index order, the order the CPU oracle restates, so outputs are
+// bit-reproducible (modes 0 and 1) and the fused argmax sees the same logits.
+#include "common.hpp"
+#include "launch.hpp"
+
+#pragma clang fp contract(off)
+
+namespace wq {
+namespace {
+
+struct GemvParams {
+    LinearArgs a;
+    ArgmaxArgs am;
+    int J;       // passes per row = ceil(K / 2048)
+    int nslots;  // row slots per workgroup = waves / J
+    int RB;      // rows per workgroup = nslots * IPW
+    int NE;      // accumulation groups per row = K / Ge
+    int NEP;     // padded LDS row stride of the group sums
+    int NG;      // weight groups per row = K / G
+};
+
+template <int MT, int MODE, int G, bool PT, int IPW, bool ARGMAX>
+__global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
+    constexpr int GE = PT ? G : 32;      // accumulation group
+    constexpr int LPG = GE / 32;         // lanes per accumulation group (1 or 4)
+    constexpr int NH = MODE == 2 ? 2 : 1;  // gate (+ up) row halves
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const LinearArgs& a = p.a;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int j = wave % p.J;
+    const int slot = wave / p.J;
+    const int64_t N = a.N;
+    const int K = (int)a.K;
+    const int RB = p.RB;
+    const int64_t r0 = (int64_t)blockIdx.x * RB;
+
+    // LDS: group sums [MT][NH][RB][NEP] i32, then scale words [NH][RB][NG] u32.
+    int32_t* acc_lds = reinterpret_cast<int32_t*>(smem);
+    uint32_t* sc_lds = reinterpret_cast<uint32_t*>(smem) + (size_t)MT * NH * RB * p.NEP;
+
+    const int kpos = kGemvPassK * j + 32 * lane;  // first code of this lane's slice
+    const bool kact = kpos < K;
+    const size_t row_bytes = (size_t)K / 2;
+    const unsigned char* wbase = reinterpret_cast<const unsigned char*>(a.wq) + (size_t)kpos / 2;
+
+    // 1. issue every weight load of this wave (rows past N re-read row N-1)
+    uint4 wv[NH][IPW];
+#pragma unroll
+    for (int s = 0; s < IPW; ++s) {
+        int64_t row = r0 + slot + (int64_t)p.nslots * s;
+        row = row < N ? row : N - 1;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            wv[h][s] = kact ? load_stream16(wbase + (size_t)(row + h * N) * row_bytes)
+                            : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    // 2. this lane's 32 activations of every token
+    uint4 xa[MT], xb[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        int64_t tt = t < a.M ? t : a.M - 1;
+        const unsigned char* xp = reinterpret_cast<const unsigned char*>(a.xq) + tt * a.K + kpos;
+        xa[t] = kact ? load16(xp) : make_uint4(0u, 0u, 0u, 0u);
+        xb[t] = kact ? load16(xp + 16) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    // 3. scale words of the workgroup's rows into LDS (contiguous per half)
+    {
+        const int per_half = RB * p.NG;
+        for (int i = tid; i < NH * per_half; i += blockDim.x) {
+            int h = i / per_half;
+            int rem = i - h * per_half;
+            int64_t row = r0 + rem / p.NG;
+            row = row < N ? row : N - 1;
+            sc_lds[i] = a.ws[(row + h * N) * p.NG + rem % p.NG];
+        }
+    }
+    // 4. exact int32 group sums -> LDS
+    const int e = kpos / GE;
+#pragma unroll
+    for (int s = 0; s < IPW; ++s) {
+        const int rl = slot + p.nslots * s;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                int d = dot32(wv[h][s], xa[t], xb[t]);
+                if (LPG == 4) d = quad_sum(d);
+                if (kact && (lane % LPG) == 0)
+                    acc_lds[((t * NH + h) * RB + rl) * p.NEP + e] = d;
+            }
+        }
+    }
+    __syncthreads();
+
+    if (a.acc_dump) {  // test hook: the group sums exactly as the epilogue reads them
+        const int rows_total = NH * (int)N;
+        for (int i = tid; i < MT * NH * RB * p.NE; i += blockDim.x) {
+            int ee = i % p.NE;
+            int rl = (i / p.NE) % RB;
+            int h = (i / (p.NE * RB)) % NH;
+            int t = i / (p.NE * RB * NH);
+            int64_t row = r0 + rl;
+            if (t < a.M && row < N)
+                a.acc_dump[((int64_t)t * rows_total + h * N + row) * p.NE + ee] =
+                    acc_lds[((t * NH + h) * RB + rl) * p.NEP + ee];
+        }
+    }
+
+    // 5. fp32 epilogue: one chain per (token, row) in group order
+    auto chain = [&](int t, int h, int rl) -> float {
+        const int32_t* ar = acc_lds + ((t * NH + h) * RB + rl) * p.NEP;
+        const uint32_t* sr = sc_lds + (h * RB + rl) * p.NG;
+        const int32_t* xsr = a.xs + (int64_t)t * p.NE;
+        float acc = 0.0f;
+        if (PT) {
+            for (int ee = 0; ee < p.NE; ++ee) {
+                uint32_t sw = sr[ee];
+                acc = fmaf(f16lo(sw), (float)ar[ee], acc);
+                acc = fmaf(f16hi(sw), (float)xsr[ee], acc);
+            }
+            return acc * a.dx[t];
+        } else {
+            const float* dr = a.dx + (int64_t)t * (K / 32);
+            for (int ee = 0; ee < p.NE; ++ee) {
+                uint32_t sw = sr[(ee * 32) / G];
+                float d = dr[ee];
+                acc = fmaf(f16lo(sw) * d, (float)ar[ee], acc);
+                acc = fmaf(f16hi(sw) * d, (float)xsr[ee], acc);
+            }
+            return acc;
+        }
+    };
+
+    if (!ARGMAX) {
+        for (int o = tid; o < MT * RB; o += blockDim.x) {
+            const int t = o / RB, rl = o - t * RB;
+            const int64_t row = r0 + rl;
+            if (t >= a.M || row >= N) continue;
+            float v = chain(t, 0, rl);
+            float* yo = a.y + (int64_t)t * N + row;
+            if (MODE == 0) {
+                *yo = v;
+            } else if (MODE == 1) {
+                *yo = *yo + v;
+            } else {
+                *yo = silu_mul(v, chain(t, 1, rl));
+            }
+        }
+        return;
+    }
+
+    // fused greedy argmax (argmax.wgsl:19-34 tie rule), one key per (t, row)
+    unsigned long long* keys = reinterpret_cast<unsigned long long*>(
+        sc_lds + (size_t)NH * RB * p.NG + 2 /* keep 8-byte alignment */);
+    keys = reinterpret_cast<unsigned long long*>((reinterpret_cast<uintptr_t>(keys) + 7) & ~uintptr_t(7));
+    __shared__ unsigned int last_block;
+    for (int o = tid; o < MT * RB; o += blockDim.x) {
+        const int t = o / RB, rl = o - t * RB;
+        const int64_t row = r0 + rl;
+        unsigned long long key = 0;
+        if (t < a.M && row < N) {
+            float v = chain(t, 0, rl);
+            if (a.y) a.y[(int64_t)t * N + row] = v;
+            if (v > -3.0e38f) key = argmax_key(v, (uint32_t)row);
+        }
+        keys[o] = key;
+    }
+    __syncthreads();
+    if (tid < MT && tid < a.M) {
+        unsigned long long best = 0;
+        for (int rl = 0; rl < RB; ++rl) best = keys[tid * RB + rl] > best ? keys[tid * RB + rl] : best;
+        if (best) atomicMax(p.am.keys + tid, best);
+        __threadfence();
+    }
+    __syncthreads();
+    if (tid == 0) {
+        unsigned int done = atomicAdd(p.am.ticket, 1u);
+        last_block = done == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (last_block) {
+        __threadfence();
+        if (tid < a.M) {
+            unsigned long long k =
+                __hip_atomic_load(p.am.keys + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            uint32_t idx = k ? 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull) : 0u;
+            p.am.tok_out[tid] = p.am.ids ? p.am.ids[idx] : idx;
+            __hip_atomic_store(p.am.keys + tid, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (tid == 0) __hip_atomic_store(p.am.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// ------------------------------------------------------------ dispatch ----
+
+struct Plan {
+    int MT, IPW, J, nslots, waves, RB, NE, NEP, NG;
+    size_t lds;
+    unsigned grid;
+};
+
+int round_tokens(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
+
+Plan make_plan(const LinearArgs& a, bool argmax) {
+    Plan p{};
+    p.MT = round_tokens(a.M);
+    const bool pt = a.GA == a.K;
+    const int ge = pt ? a.G : 32;
+    p.J = (int)((a.K + kGemvPassK - 1) / kGemvPassK);
+    p.nslots = p.J >= 4 ? 1 : (4 + p.J - 1) / p.J;
+    p.waves = p.J * p.nslots;
+    p.NE = (int)(a.K / ge);
+    p.NEP = p.NE + 1;
+    p.NG = (int)(a.K / a.G);
+    const int nh = a.mode == 2 ? 2 : 1;
+    // rows per wave: enough workgroups to cover 256 CUs, at most 8 loads each
+    const int64_t cus = 256;
+    int ipw = 8;
+    static const int choices[] = {1, 2, 4, 6, 8};
+    for (int c : choices) {
+        int64_t rb = (int64_t)p.nslots * c;
+        if ((a.N + rb - 1) / rb <= cus * 1) { ipw = c; break; }
+    }
+    // LDS budget: 64 KiB per workgroup
+    auto lds_of = [&](int ipw_) {
+        size_t rb = (size_t)p.nslots * ipw_;
+        size_t b = (size_t)p.MT * nh * rb * p.NEP * 4 + (size_t)nh * rb * p.NG * 4;
+        if (argmax) b += 16 + (size_t)p.MT * rb * 8;
+        return b;
+    };
+    while (ipw > 1 && lds_of(ipw) > 65536) ipw = ipw == 8 ? 6 : ipw == 6 ? 4 : ipw / 2;
+    p.IPW = ipw;
+    p.RB = p.nslots * ipw;
+    p.lds = lds_of(ipw);
+    p.grid = (unsigned)((a.N + p.RB - 1) / p.RB);
+    return p;
+}
+
+template <int MT, int MODE, int G, bool PT, bool ARGMAX>
+hipError_t launch_ipw(const Plan& pl, const GemvParams& gp, hipStream_t s) {
+    dim3 grid(pl.grid), block(64 * pl.waves);
+    switch (pl.IPW) {
+        case 1: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 1, ARGMAX>), grid, block, pl.lds, s, gp); break;
+        case 2: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 2, ARGMAX>), grid, block, pl.lds, s, gp); break;
+        case 4: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 4, ARGMAX>), grid, block, pl.lds, s, gp); break;
+        case 6: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 6, ARGMAX>), grid, block, pl.lds, s, gp); break;
+        default: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 8, ARGMAX>), grid, block, pl.lds, s, gp); break;
+    }
+    return hipGetLastError();
+}
+
+template <int MT, int MODE, bool ARGMAX>
+hipError_t launch_gpt(const Plan& pl, const GemvParams& gp, hipStream_t s) {
+    const bool pt = gp.a.GA == gp.a.K;
+    if (gp.a.G == 128) {
+        return pt ? launch_ipw<MT, MODE, 128, true, ARGMAX>(pl, gp, s)
+                  : launch_ipw<MT, MODE, 128, false, ARGMAX>(pl, gp, s);
+    }
+    return pt ? launch_ipw<MT, MODE, 32, true, ARGMAX>(pl, gp, s)
+              : launch_ipw<MT, MODE, 32, false, ARGMAX>(pl, gp, s);
+}
+
+template <int MODE, bool ARGMAX>
+hipError_t launch_mt(const Plan& pl, const GemvParams& gp, hipStream_t s) {
+    switch (pl.MT) {
+        case 1: return launch_gpt<1, MODE, ARGMAX>(pl, gp, s);
+        case 2: return launch_gpt<2, MODE, ARGMAX>(pl, gp, s);
+        case 4: return launch_gpt<4, MODE, ARGMAX>(pl, gp, s);
+        default: return launch_gpt<8, MODE, ARGMAX>(pl, gp, s);
+    }
+}
+
+GemvParams params_of(const LinearArgs& a, const Plan& pl) {
+    GemvParams gp{};
+    gp.a = a;
+    gp.J = pl.J;
+    gp.nslots = pl.nslots;
+    gp.RB = pl.RB;
+    gp.NE = pl.NE;
+    gp.NEP = pl.NEP;
+    gp.NG = pl.NG;
+    return gp;
+}
+
+}  // namespace
+
+hipError_t launch_gemv(const LinearArgs& a, hipStream_t s) {
+    Plan pl = make_plan(a, false);
+    GemvParams gp = params_of(a, pl);
+    switch (a.mode) {
+        case 0: return launch_mt<0, false>(pl, gp, s);
+        case 1: return launch_mt<1, false>(pl, gp, s);
+        default: return launch_mt<2, false>(pl, gp, s);
+    }
+}
+
+hipError_t launch_lm_head_argmax(const LinearArgs& a, const ArgmaxArgs& am, hipStream_t s) {
+    Plan pl = make_plan(a, true);
+    GemvParams gp = params_of(a, pl);
+    gp.am = am;
+    return launch_mt<0, true>(pl, gp, s);
+}
+
+}  // namespace wq

@@ -1,0 +1,58 @@
+// Internal launcher interface between the C-ABI layer (capi.hip) and the
+// kernel translation units.  Arguments are already validated by the caller.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wq {
+
+struct QuantArgs {
+    const float* x;
+    const float* norm_w;  // nullable: RMSNorm prologue when set
+    float eps;
+    int64_t M, K;
+    int GA, G;  // GA: K (per token) or 32; xs group Ge = min(G, GA)
+    int8_t* xq;
+    float* dx;
+    int32_t* xs;
+};
+
+struct LinearArgs {
+    const uint32_t* wq;  // [rows, K/8], rows = N (2N for mode 2)
+    const uint32_t* ws;  // [rows, K/G]
+    int64_t N, K;
+    int G;
+    const int8_t* xq;  // [M, K]
+    const float* dx;   // [M, K/GA]
+    const int32_t* xs; // [M, K/Ge]
+    int64_t M;
+    int GA;
+    int mode;
+    float* y;            // [M, N]; nullable only for the lm_head argmax path
+    int32_t* acc_dump;   // nullable: [M, rows, K/Ge] int32 group accumulators
+};
+
+struct ArgmaxArgs {
+    const uint32_t* ids;  // nullable id map (draft vocabulary)
+    uint32_t* tok_out;    // [M]
+    unsigned long long* keys;  // workspace: [8] running (value, index) keys
+    unsigned int* ticket;      // workspace: blocks-finished counter
+};
+
+hipError_t launch_quant_act(const QuantArgs& a, hipStream_t s);
+hipError_t launch_gemv(const LinearArgs& a, hipStream_t s);
+hipError_t launch_lm_head_argmax(const LinearArgs& a, const ArgmaxArgs& am, hipStream_t s);
+hipError_t launch_gemm(const LinearArgs& a, hipStream_t s);
+hipError_t launch_argmax(const float* logits, int64_t M, int64_t V, const uint32_t* ids,
+                         uint32_t* tok_out, hipStream_t s);
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
+
+// Decode GEMV: rows of one pass = 1 KiB of packed weights = 2048 codes.
+constexpr int kGemvPassK = 2048;
+// Largest token count of the decode GEMV (the M <= 8 speculative-verify case).
+constexpr int kGemvMaxTokens = 8;
+// Workspace of the fused lm_head argmax: 8 keys + ticket, padded.
+constexpr size_t kArgmaxWorkspaceBytes = 128;
+
+}  // namespace wq
