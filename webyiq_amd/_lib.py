@@ -57,6 +57,15 @@ class WqError(RuntimeError):
 _lib = None
 
 
+def _hip_runtimes():
+    """Paths of the libamdhip64 images mapped into this process."""
+    try:
+        with open("/proc/self/maps") as f:
+            return sorted({l.split()[-1] for l in f if "libamdhip64" in l})
+    except OSError:
+        return []
+
+
 def load():
     """Load the HIP library (raises if it has not been built)."""
     global _lib
@@ -65,7 +74,15 @@ def load():
             raise RuntimeError(
                 f"{LIB_PATH} is missing: build it with `python -m webyiq_amd.build` "
                 "(the int4 x int8 path has no CPU fallback)")
+        # torch bundles its own libamdhip64.so (soname libamdhip64.so.7).  Loading
+        # it first makes this library bind to that same runtime instance; loading
+        # ours first would map /opt/rocm's copy too, and a second HIP runtime in
+        # one process finds no device.
+        import torch  # noqa: F401
         lib = ctypes.CDLL(LIB_PATH)
+        runtimes = _hip_runtimes()
+        if len(runtimes) > 1:
+            raise RuntimeError(f"two HIP runtimes mapped in this process: {runtimes}")
         for name, (args, res) in PROTOTYPES.items():
             f = getattr(lib, name)
             f.argtypes = args
