@@ -3,9 +3,12 @@ on the same seeded inputs.
 
 Bars (stated per test):
   * int8 codes, dx, xs, int32 group sums, argmax tokens: bit-exact;
-  * fp32 outputs of modes 0/1: bit-exact against the oracle's canonical fold
+  * GEMV fp32 outputs of modes 0/1, and GEMM outputs of the group-32 /
+    per-32-activation formats: bit-exact against the oracle's canonical fold
     (one fma chain per output over the groups in order);
-  * mode 2 (SiLU): within 1e-5 of the oracle (device expf vs libm expf);
+  * GEMM outputs of the per-token group-128 format, which folds the min term
+    separately on an f16 MFMA, and mode 2 (device expf vs libm expf): within
+    rel 1e-5 (max-norm) of the oracle;
   * every fp32 output within rel 1e-3 (max-norm) of the torch fake-quant path.
 """
 import numpy as np
@@ -140,6 +143,9 @@ GEMM_CASES = [
     (17, 512, 64, 32, None, 1),
     (48, 1024, 128, 128, 32, 2),
     (1, 128, 16, 128, None, 0),
+    (200, 2048, 320, 128, None, 2),   # mode 2 at width 256
+    (129, 1024, 130, 32, None, 0),
+    (300, 6144, 2048, 128, None, 1),  # down-projection shape, tile width 64
 ]
 
 
@@ -158,7 +164,7 @@ def test_gemm_bit_exact(M, K, N, G, GA, mode):
     y, acc = ops.group_sums(ops.PATH_PREFILL, w, a, mode=mode, y=dev(y0) if mode == 1 else None)
     assert np.array_equal(host(acc), acc_want)
     got = host(y)
-    if mode == 2:
+    if mode == 2 or (G == 128 and GA is None):
         assert rel_err(got, want) < 1e-5
     else:
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
@@ -168,8 +174,8 @@ def test_gemm_bit_exact(M, K, N, G, GA, mode):
 
 def test_gemm_matches_gemv_rows():
     """Decode vs prefill cross-check (the reference's --ppl / --sequential
-    harnesses, crates/cli/src/main.rs:209-250): each GEMM row equals the GEMV
-    of that token, bit for bit."""
+    harnesses, crates/cli/src/main.rs:209-250): each GEMM row matches the GEMV
+    of that token to rel 1e-5 (the GEMM folds the min term on an f16 MFMA)."""
     note("gemm vs gemv rows")
     M, K, N = 40, 2048, 1024
     wq, ws, x, xq, dx, xs = setup_linear(5, M, K, N, 128, None)
@@ -179,7 +185,7 @@ def test_gemm_matches_gemv_rows():
     for t0 in range(0, M, 8):
         sub = dev_acts(xq[t0:t0 + 8], dx[t0:t0 + 8], xs[t0:t0 + 8], K, 128)
         yv = host(ops.matmul(ops.PATH_SPEC, w, sub))
-        assert np.array_equal(yv, yg[t0:t0 + 8])
+        assert rel_err(yg[t0:t0 + 8], yv) < 1e-5
 
 
 # -------------------------------------------------------------- argmax ------

@@ -67,6 +67,15 @@ __device__ __forceinline__ uint4 load16(const void* p) {
     return *reinterpret_cast<const uint4*>(p);
 }
 
+// Force a kernel argument into registers at this point.  Scalar loads of
+// kernel arguments are otherwise sunk next to their first use, and one issued
+// after the main memory wait adds a whole memory round trip to the critical
+// path of a latency-bound kernel.
+template <typename T>
+__device__ __forceinline__ void pin_arg(const T& v) {
+    asm volatile("" ::"s"(v));
+}
+
 // SiLU(a) * u in the reference's form a / (1 + exp(-a)) * u
 // (crates/engine/src/shaders/gemv_q4q8.wgsl:128).
 __device__ __forceinline__ float silu_mul(float a, float u) {

@@ -36,69 +36,106 @@ struct GemvParams {
     int NE;      // accumulation groups per row = K / Ge
     int NEP;     // padded LDS row stride of the group sums
     int NG;      // weight groups per row = K / G
+    int nblocks; // gridDim.x
 };
 
 template <int MT, int MODE, int G, bool PT, int IPW, bool ARGMAX>
-__global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
-    constexpr int GE = PT ? G : 32;      // accumulation group
-    constexpr int LPG = GE / 32;         // lanes per accumulation group (1 or 4)
+__global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
+    constexpr int GE = PT ? G : 32;        // accumulation group
+    constexpr int LPG = GE / 32;           // lanes per accumulation group (1 or 4)
+    constexpr int LPW = G / 32;            // lanes per weight group (1 or 4)
     constexpr int NH = MODE == 2 ? 2 : 1;  // gate (+ up) row halves
     extern __shared__ __align__(16) unsigned char smem[];
 
     const LinearArgs& a = p.a;
+    // every kernel argument in SGPRs before the first global load
+    pin_arg(a.wq); pin_arg(a.ws); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs); pin_arg(a.y);
+    pin_arg(a.acc_dump); pin_arg(a.N); pin_arg(a.K); pin_arg(a.M);
+    pin_arg(p.J); pin_arg(p.nslots); pin_arg(p.RB); pin_arg(p.NE); pin_arg(p.NEP); pin_arg(p.NG);
+    if (ARGMAX) {
+        pin_arg(p.am.ids); pin_arg(p.am.tok_out); pin_arg(p.am.keys); pin_arg(p.am.ticket);
+        pin_arg(p.nblocks);
+    }
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    const int NW = p.J * p.nslots;  // waves (blockDim.x / 64, without its late scalar load)
+    const int nthreads = 64 * NW;
     const int j = wave % p.J;
     const int slot = wave / p.J;
     const int64_t N = a.N;
     const int K = (int)a.K;
     const int RB = p.RB;
+    const int NE = p.NE, NEP = p.NEP, NG = p.NG;
+    const int NDX = PT ? 1 : K / 32;
     const int64_t r0 = (int64_t)blockIdx.x * RB;
 
-    // LDS: group sums [MT][NH][RB][NEP] i32, then scale words [NH][RB][NG] u32.
+    // LDS: group sums [MT][NH][RB][NEP] i32 | weight (s, m) [NH][RB][NG] f32x2 |
+    //      activation sums [MT][NE] f32 | activation scales [MT][NDX] f32
     int32_t* acc_lds = reinterpret_cast<int32_t*>(smem);
-    uint32_t* sc_lds = reinterpret_cast<uint32_t*>(smem) + (size_t)MT * NH * RB * p.NEP;
+    float2* sm_lds = reinterpret_cast<float2*>(acc_lds + (size_t)MT * NH * RB * NEP);
+    float* xs_lds = reinterpret_cast<float*>(sm_lds + (size_t)NH * RB * NG);
+    float* dx_lds = xs_lds + (size_t)MT * NE;
 
-    const int kpos = kGemvPassK * j + 32 * lane;  // first code of this lane's slice
-    const bool kact = kpos < K;
+    // Lanes past the end of a partial pass (K % 2048 != 0) load from position 0
+    // and never write their results: every load below is unconditional, so no
+    // branch can hold a wait that would serialise a second memory round trip.
+    const int kraw = kGemvPassK * j + 32 * lane;  // first code of this lane's slice
+    const bool kact = kraw < K;
+    const int kpos = kact ? kraw : 0;
+    const int e = kpos / GE;  // this lane's accumulation group
+    const int g = kpos / G;   // this lane's weight group
     const size_t row_bytes = (size_t)K / 2;
     const unsigned char* wbase = reinterpret_cast<const unsigned char*>(a.wq) + (size_t)kpos / 2;
 
-    // 1. issue every weight load of this wave (rows past N re-read row N-1)
+    // 1. issue every global load of this lane before the first one is consumed
+    //    (one memory round trip; rows past N re-read row N-1)
     uint4 wv[NH][IPW];
+    uint32_t sv[NH][IPW];
 #pragma unroll
     for (int s = 0; s < IPW; ++s) {
         int64_t row = r0 + slot + (int64_t)p.nslots * s;
         row = row < N ? row : N - 1;
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
-            wv[h][s] = kact ? load_stream16(wbase + (size_t)(row + h * N) * row_bytes)
-                            : make_uint4(0u, 0u, 0u, 0u);
+            wv[h][s] = load_stream16(wbase + (size_t)(row + h * N) * row_bytes);
+            sv[h][s] = a.ws[(row + h * N) * NG + g];
         }
     }
-    // 2. this lane's 32 activations of every token
     uint4 xa[MT], xb[MT];
+    int32_t xsv[MT];
+    float dxv[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
         int64_t tt = t < a.M ? t : a.M - 1;
         const unsigned char* xp = reinterpret_cast<const unsigned char*>(a.xq) + tt * a.K + kpos;
-        xa[t] = kact ? load16(xp) : make_uint4(0u, 0u, 0u, 0u);
-        xb[t] = kact ? load16(xp + 16) : make_uint4(0u, 0u, 0u, 0u);
+        xa[t] = load16(xp);
+        xb[t] = load16(xp + 16);
+        xsv[t] = a.xs[tt * NE + e];
+        dxv[t] = a.dx[tt * NDX + (PT ? 0 : e)];
     }
-    // 3. scale words of the workgroup's rows into LDS (contiguous per half)
-    {
-        const int per_half = RB * p.NG;
-        for (int i = tid; i < NH * per_half; i += blockDim.x) {
-            int h = i / per_half;
-            int rem = i - h * per_half;
-            int64_t row = r0 + rem / p.NG;
-            row = row < N ? row : N - 1;
-            sc_lds[i] = a.ws[(row + h * N) * p.NG + rem % p.NG];
+
+    // 2. activation sums / scales and weight (s, m) -> LDS
+    if (slot == 0 && kact && (lane % LPG) == 0) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            xs_lds[t * NE + e] = (float)xsv[t];
+            if (!PT) dx_lds[t * NDX + e] = dxv[t];
         }
     }
-    // 4. exact int32 group sums -> LDS
-    const int e = kpos / GE;
+    if (PT && tid == 0) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) dx_lds[t] = dxv[t];
+    }
+    if (kact && (lane % LPW) == 0) {
+#pragma unroll
+        for (int s = 0; s < IPW; ++s)
+#pragma unroll
+            for (int h = 0; h < NH; ++h)
+                sm_lds[(h * RB + slot + p.nslots * s) * NG + g] = make_float2(f16lo(sv[h][s]), f16hi(sv[h][s]));
+    }
+
+    // 3. exact int32 group sums -> LDS
 #pragma unroll
     for (int s = 0; s < IPW; ++s) {
         const int rl = slot + p.nslots * s;
@@ -108,8 +145,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
             for (int t = 0; t < MT; ++t) {
                 int d = dot32(wv[h][s], xa[t], xb[t]);
                 if (LPG == 4) d = quad_sum(d);
-                if (kact && (lane % LPG) == 0)
-                    acc_lds[((t * NH + h) * RB + rl) * p.NEP + e] = d;
+                if (kact && (lane % LPG) == 0) acc_lds[((t * NH + h) * RB + rl) * NEP + e] = d;
             }
         }
     }
@@ -117,45 +153,46 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
 
     if (a.acc_dump) {  // test hook: the group sums exactly as the epilogue reads them
         const int rows_total = NH * (int)N;
-        for (int i = tid; i < MT * NH * RB * p.NE; i += blockDim.x) {
-            int ee = i % p.NE;
-            int rl = (i / p.NE) % RB;
-            int h = (i / (p.NE * RB)) % NH;
-            int t = i / (p.NE * RB * NH);
+        for (int i = tid; i < MT * NH * RB * NE; i += nthreads) {
+            int ee = i % NE;
+            int rl = (i / NE) % RB;
+            int h = (i / (NE * RB)) % NH;
+            int t = i / (NE * RB * NH);
             int64_t row = r0 + rl;
             if (t < a.M && row < N)
-                a.acc_dump[((int64_t)t * rows_total + h * N + row) * p.NE + ee] =
-                    acc_lds[((t * NH + h) * RB + rl) * p.NEP + ee];
+                a.acc_dump[((int64_t)t * rows_total + h * N + row) * NE + ee] =
+                    acc_lds[((t * NH + h) * RB + rl) * NEP + ee];
         }
     }
 
-    // 5. fp32 epilogue: one chain per (token, row) in group order
+    // 4. fp32 epilogue: one chain per (token, row) over the groups in order
     auto chain = [&](int t, int h, int rl) -> float {
-        const int32_t* ar = acc_lds + ((t * NH + h) * RB + rl) * p.NEP;
-        const uint32_t* sr = sc_lds + (h * RB + rl) * p.NG;
-        const int32_t* xsr = a.xs + (int64_t)t * p.NE;
+        const int32_t* ar = acc_lds + ((t * NH + h) * RB + rl) * NEP;
+        const float2* sr = sm_lds + (h * RB + rl) * NG;
+        const float* xsr = xs_lds + t * NE;
+        const float* dr = dx_lds + t * NDX;
         float acc = 0.0f;
         if (PT) {
-            for (int ee = 0; ee < p.NE; ++ee) {
-                uint32_t sw = sr[ee];
-                acc = fmaf(f16lo(sw), (float)ar[ee], acc);
-                acc = fmaf(f16hi(sw), (float)xsr[ee], acc);
+#pragma unroll 8
+            for (int ee = 0; ee < NE; ++ee) {
+                float2 w = sr[ee];
+                acc = fmaf(w.x, (float)ar[ee], acc);
+                acc = fmaf(w.y, xsr[ee], acc);
             }
-            return acc * a.dx[t];
+            return acc * dr[0];
         } else {
-            const float* dr = a.dx + (int64_t)t * (K / 32);
-            for (int ee = 0; ee < p.NE; ++ee) {
-                uint32_t sw = sr[(ee * 32) / G];
+#pragma unroll 8
+            for (int ee = 0; ee < NE; ++ee) {
+                float2 w = sr[(ee * 32) / G];
                 float d = dr[ee];
-                acc = fmaf(f16lo(sw) * d, (float)ar[ee], acc);
-                acc = fmaf(f16hi(sw) * d, (float)xsr[ee], acc);
+                acc = fmaf(w.x * d, (float)ar[ee], acc);
+                acc = fmaf(w.y * d, xsr[ee], acc);
             }
             return acc;
         }
     };
-
     if (!ARGMAX) {
-        for (int o = tid; o < MT * RB; o += blockDim.x) {
+        for (int o = tid; o < MT * RB; o += nthreads) {
             const int t = o / RB, rl = o - t * RB;
             const int64_t row = r0 + rl;
             if (t >= a.M || row >= N) continue;
@@ -174,10 +211,9 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
 
     // fused greedy argmax (argmax.wgsl:19-34 tie rule), one key per (t, row)
     unsigned long long* keys = reinterpret_cast<unsigned long long*>(
-        sc_lds + (size_t)NH * RB * p.NG + 2 /* keep 8-byte alignment */);
-    keys = reinterpret_cast<unsigned long long*>((reinterpret_cast<uintptr_t>(keys) + 7) & ~uintptr_t(7));
+        (reinterpret_cast<uintptr_t>(dx_lds + (size_t)MT * NDX) + 7) & ~uintptr_t(7));
     __shared__ unsigned int last_block;
-    for (int o = tid; o < MT * RB; o += blockDim.x) {
+    for (int o = tid; o < MT * RB; o += nthreads) {
         const int t = o / RB, rl = o - t * RB;
         const int64_t row = r0 + rl;
         unsigned long long key = 0;
@@ -198,7 +234,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
     __syncthreads();
     if (tid == 0) {
         unsigned int done = atomicAdd(p.am.ticket, 1u);
-        last_block = done == gridDim.x - 1;
+        last_block = done == (unsigned)p.nblocks - 1;
     }
     __syncthreads();
     if (last_block) {
@@ -222,6 +258,11 @@ struct Plan {
     unsigned grid;
 };
 
+#ifndef WQ_GEMV_TARGET_WGS
+#define WQ_GEMV_TARGET_WGS 256
+#endif
+constexpr int64_t kGemvTargetWgs = WQ_GEMV_TARGET_WGS;  // MI355X: 256 CUs
+
 int round_tokens(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
 Plan make_plan(const LinearArgs& a, bool argmax) {
@@ -233,25 +274,29 @@ Plan make_plan(const LinearArgs& a, bool argmax) {
     p.nslots = p.J >= 4 ? 1 : (4 + p.J - 1) / p.J;
     p.waves = p.J * p.nslots;
     p.NE = (int)(a.K / ge);
-    p.NEP = p.NE + 1;
+    p.NEP = (p.NE + 4) & ~3;  // 16-byte rows, spread over LDS banks
     p.NG = (int)(a.K / a.G);
     const int nh = a.mode == 2 ? 2 : 1;
-    // rows per wave: enough workgroups to cover 256 CUs, at most 8 loads each
-    const int64_t cus = 256;
+    // rows per wave: the fewest loads per lane that still keep the grid within
+    // kGemvTargetWgs workgroups (every CU busy, all loads issued up front)
     int ipw = 8;
     static const int choices[] = {1, 2, 4, 6, 8};
     for (int c : choices) {
         int64_t rb = (int64_t)p.nslots * c;
-        if ((a.N + rb - 1) / rb <= cus * 1) { ipw = c; break; }
+        if ((a.N + rb - 1) / rb <= kGemvTargetWgs) { ipw = c; break; }
     }
     // LDS budget: 64 KiB per workgroup
     auto lds_of = [&](int ipw_) {
         size_t rb = (size_t)p.nslots * ipw_;
-        size_t b = (size_t)p.MT * nh * rb * p.NEP * 4 + (size_t)nh * rb * p.NG * 4;
+        size_t b = (size_t)p.MT * nh * rb * p.NEP * 4 + (size_t)nh * rb * p.NG * 8 +
+                   (size_t)p.MT * p.NE * 4 + (size_t)p.MT * (pt ? 1 : a.K / 32) * 4;
         if (argmax) b += 16 + (size_t)p.MT * rb * 8;
         return b;
     };
-    while (ipw > 1 && lds_of(ipw) > 65536) ipw = ipw == 8 ? 6 : ipw == 6 ? 4 : ipw / 2;
+    // registers: weights in flight (4 per row half) + activations (8 per token)
+    auto regs_of = [&](int ipw_) { return nh * ipw_ * 4 + 8 * p.MT; };
+    while (ipw > 1 && (lds_of(ipw) > 65536 || regs_of(ipw) > 96))
+        ipw = ipw == 8 ? 6 : ipw == 6 ? 4 : ipw / 2;
     p.IPW = ipw;
     p.RB = p.nslots * ipw;
     p.lds = lds_of(ipw);
@@ -302,6 +347,7 @@ GemvParams params_of(const LinearArgs& a, const Plan& pl) {
     gp.NE = pl.NE;
     gp.NEP = pl.NEP;
     gp.NG = pl.NG;
+    gp.nblocks = (int)pl.grid;
     return gp;
 }
 

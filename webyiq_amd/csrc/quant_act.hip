@@ -38,24 +38,46 @@ __device__ float sqrt_rn(float x) {
     return r;
 }
 
-template <bool NORM, bool PER_TOKEN, int GE>
+// Up to kCacheChunks float4 per thread stay in registers (K <= 8192): the row
+// is read from memory once; longer rows are re-read (L2 hits) per pass.
+constexpr int kCacheChunks = 8;
+
+template <bool NORM, bool PER_TOKEN, int GE, bool CACHED>
 __global__ __launch_bounds__(kQuantThreads) void quant_act_kernel(QuantArgs a) {
+    pin_arg(a.x); pin_arg(a.norm_w); pin_arg(a.eps); pin_arg(a.K);
+    pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
     const int tid = threadIdx.x;
     const int64_t t = blockIdx.x;
     const int K = (int)a.K;
     const int nchunk = K / 4;
     const int jmax = (nchunk + kQuantThreads - 1) / kQuantThreads;
+    const int JL = CACHED ? kCacheChunks : jmax;  // constant trip count when cached
     const float4* xr = reinterpret_cast<const float4*>(a.x + t * a.K);
     const float4* nw = reinterpret_cast<const float4*>(a.norm_w);
     __shared__ float red[kQuantThreads];
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+
+    // one round of loads: the whole row (and norm weight) for this thread
+    float4 xc[CACHED ? kCacheChunks : 1], wc[CACHED && NORM ? kCacheChunks : 1];
+    if (CACHED) {
+#pragma unroll
+        for (int j = 0; j < kCacheChunks; ++j) {
+            int c = tid + kQuantThreads * j;
+            bool ok = j < jmax && c < nchunk;
+            xc[j] = ok ? xr[c] : zero4;
+            if (NORM) wc[j] = ok ? nw[c] : zero4;
+        }
+    }
+    auto raw = [&](int j, int c) -> float4 { return CACHED ? xc[CACHED ? j : 0] : xr[c]; };
 
     float r = 1.0f;
     if (NORM) {
         float p = 0.0f;
-        for (int j = 0; j < jmax; ++j) {
+#pragma unroll
+        for (int j = 0; j < JL; ++j) {
             int c = tid + kQuantThreads * j;
-            if (c < nchunk) {
-                float4 v = xr[c];
+            if (j < jmax && c < nchunk) {
+                float4 v = raw(j, c);
                 p = fmaf(v.x, v.x, p);
                 p = fmaf(v.y, v.y, p);
                 p = fmaf(v.z, v.z, p);
@@ -72,10 +94,10 @@ __global__ __launch_bounds__(kQuantThreads) void quant_act_kernel(QuantArgs a) {
         __syncthreads();
     }
 
-    auto load = [&](int c) -> float4 {
-        float4 v = xr[c];
+    auto load = [&](int j, int c) -> float4 {
+        float4 v = raw(j, c);
         if (NORM) {
-            float4 w = nw[c];
+            float4 w = CACHED ? wc[CACHED && NORM ? j : 0] : nw[c];
             v.x = (v.x * r) * w.x;
             v.y = (v.y * r) * w.y;
             v.z = (v.z * r) * w.z;
@@ -88,10 +110,11 @@ __global__ __launch_bounds__(kQuantThreads) void quant_act_kernel(QuantArgs a) {
     float dtok = 0.0f;
     if (PER_TOKEN) {
         float m = 0.0f;
-        for (int j = 0; j < jmax; ++j) {
+#pragma unroll
+        for (int j = 0; j < JL; ++j) {
             int c = tid + kQuantThreads * j;
-            if (c < nchunk) {
-                float4 v = load(c);
+            if (j < jmax && c < nchunk) {
+                float4 v = load(j, c);
                 m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
             }
         }
@@ -106,10 +129,12 @@ __global__ __launch_bounds__(kQuantThreads) void quant_act_kernel(QuantArgs a) {
 
     uint32_t* xq = reinterpret_cast<uint32_t*>(a.xq + t * a.K);
     constexpr int kLanesPerGe = GE / 4;  // lanes (float4 chunks) per xs group
-    for (int j = 0; j < jmax; ++j) {
+#pragma unroll
+    for (int j = 0; j < JL; ++j) {
+        if (j >= jmax) break;
         int c = tid + kQuantThreads * j;
         bool valid = c < nchunk;
-        float4 v = valid ? load(c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 v = valid ? load(j, c) : zero4;
         float d = dtok;
         if (!PER_TOKEN) {
             // 32-element activation group = 8 consecutive lanes
@@ -134,24 +159,26 @@ __global__ __launch_bounds__(kQuantThreads) void quant_act_kernel(QuantArgs a) {
     }
 }
 
-template <bool NORM>
+template <bool NORM, bool CACHED>
 hipError_t dispatch_quant(const QuantArgs& a, hipStream_t s) {
     dim3 grid((unsigned)a.M), block(kQuantThreads);
     bool pt = a.GA == a.K;
     int ge = a.GA < a.G ? a.GA : a.G;
     if (pt && ge == 128)
-        hipLaunchKernelGGL((quant_act_kernel<NORM, true, 128>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((quant_act_kernel<NORM, true, 128, CACHED>), grid, block, 0, s, a);
     else if (pt && ge == 32)
-        hipLaunchKernelGGL((quant_act_kernel<NORM, true, 32>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((quant_act_kernel<NORM, true, 32, CACHED>), grid, block, 0, s, a);
     else
-        hipLaunchKernelGGL((quant_act_kernel<NORM, false, 32>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((quant_act_kernel<NORM, false, 32, CACHED>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_quant_act(const QuantArgs& a, hipStream_t s) {
-    return a.norm_w ? dispatch_quant<true>(a, s) : dispatch_quant<false>(a, s);
+    const bool cached = a.K <= 4 * kQuantThreads * kCacheChunks;
+    if (a.norm_w) return cached ? dispatch_quant<true, true>(a, s) : dispatch_quant<true, false>(a, s);
+    return cached ? dispatch_quant<false, true>(a, s) : dispatch_quant<false, false>(a, s);
 }
 
 }  // namespace wq
