@@ -168,8 +168,47 @@ def test_gemm_bit_exact(M, K, N, G, GA, mode):
         assert rel_err(got, want) < 1e-5
     else:
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the plain entry point (its own tile width) computes the same values
+    y2 = host(ops.gemm(w, a, mode=mode, y=dev(y0) if mode == 1 else None))
+    assert np.array_equal(y2.view(np.uint32), got.view(np.uint32))
     fq = ref.FakeQuantLinear(wq, ws, K, G, mode=mode, GA=GA)(x, y0).numpy()
     assert rel_err(got, fq) < 1e-3
+
+
+# tile width the launcher picks for M = 1024 (8 tiles along M): 192, 256, 128,
+# 256 (mode 2), 64; the other formats at width 128
+WIDE_CASES = [
+    (2048, 6144, 128, None, 0),
+    (2048, 8192, 128, None, 0),
+    (2048, 4096, 128, None, 0),
+    (2048, 4096, 128, None, 2),
+    (6144, 2048, 128, None, 1),
+    (2048, 4096, 32, None, 0),
+    (2048, 4096, 128, 32, 1),
+]
+
+
+@pytest.mark.parametrize("K,N,G,GA,mode", WIDE_CASES)
+def test_gemm_wide_tiles(K, N, G, GA, mode):
+    """Prefill shapes (M = 1024) on the production tile widths, checked on 24
+    sampled tokens that span every tile row against the oracle."""
+    M = 1024
+    note(f"gemm wide M={M} K={K} N={N} G={G} GA={GA} mode={mode}")
+    rows = 2 * N if mode == 2 else N
+    wq, ws, x, xq, dx, xs = setup_linear(K + N + G + mode, M, K, rows, G, GA)
+    gaa = K if GA is None else GA
+    y0 = np.random.default_rng(3).normal(size=(M, N)).astype(np.float32) if mode == 1 else None
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
+    a = dev_acts(xq, dx, xs, gaa, G)
+    got = host(ops.gemm(w, a, mode=mode, y=dev(y0) if mode == 1 else None))
+    idx = np.unique(np.concatenate([np.arange(0, M, 64), np.arange(63, M, 128)]))
+    want = orc.linear(wq, ws, K, G, xq[idx], dx[idx], xs[idx], mode=mode,
+                      y=y0[idx] if mode == 1 else None, GA=gaa)
+    if mode == 2 or (G == 128 and GA is None):
+        assert rel_err(got[idx], want) < 1e-5
+    else:
+        assert np.array_equal(got[idx].view(np.uint32), want.view(np.uint32))
+    assert np.all(np.isfinite(got))
 
 
 def test_gemm_matches_gemv_rows():

@@ -6,6 +6,9 @@ Each .hip translation unit is compiled in parallel into webyiq_amd/_build/,
 then linked into webyiq_amd/libwebyiq_q4q8.so next to this file.  Flags:
   --offload-arch=gfx950 only (no other targets, no CUDA/HIP dual paths);
   -Xclang -target-feature -Xclang -packed-fp32-ops: no packed fp32 ops;
+  -mllvm -amdgpu-mfma-vgpr-form: MFMA results in ordinary VGPRs, which the
+  VALU epilogues read directly (accumulation registers would need a copy
+  instruction per element);
   no fast-math: divisions and the fp32 epilogues keep IEEE semantics that
   the CPU oracle reproduces bit for bit.
 """
@@ -27,6 +30,7 @@ CFLAGS = [
     "-fPIC",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -6,25 +6,27 @@
 // y[t,n] = dx[t] * sum_g (s[n,g] * A[t,n,g] + m[n,g] * X[t,g]),
 // A = exact int32 sum of q * xq over group g, X = sum of xq over g.
 //
-// MI355X design.  A workgroup of 8 waves (2 along M x 4 along N, two waves per
-// SIMD so one wave's VALU fold overlaps the other's MFMAs) owns a 128-token x
-// BN-row tile; BN is chosen by the host so that the grid covers the 256 CUs.
-// Per K step of 128 codes the int8 activation tile (128 x 128 B) and the
-// packed int4 weight tile (BN x 64 B) go global -> registers -> LDS into one of
-// two buffers while the other buffer feeds the MFMAs: one barrier per step.
-// Each wave reads its weight fragments packed (8 B = 16 codes per lane),
-// expands nibbles to int8 in registers and issues v_mfma_i32_16x16x64_i8
-// (16x16x32 for 32-code groups).  The int32 group sums are exact.
+// MI355X design.  A workgroup of 4 waves (2 along M x 2 along N, one per SIMD)
+// owns a 128-token x BN-row tile, and each wave a 64 x BN/2 block of 32 x 32
+// subtiles computed with v_mfma_i32_32x32x32_i8 (the full-rate int8 MFMA on
+// gfx950; the 16x16x64 form runs at half rate).  Every tile of a K step (128
+// codes) travels global -> LDS directly (global_load_lds, no registers): the
+// int8 activations, the packed int4 weights, the scale words.  A ring of 4
+// LDS stages keeps 3 steps in flight; each step ends with one barrier,
+// preceded by a wait for exactly the loads of the next step.  Each wave
+// expands its weight fragments from nibbles to int8 in registers.  Tiles
+// are stored in rows whose 16-byte chunks are XOR-swizzled by the row index,
+// so that the 16-byte fragment reads of consecutive rows hit distinct banks.
 //
-// Folding the group sums into fp32 is VALU work per output element per group
-// (it costs as much as the MFMAs), so the per-token group-128 format keeps it
-// at two instructions, acc = fma(s, float(A), acc), and moves the min term
-// sum_g m * X onto an f16 MFMA at the start: X = 64 * X_hi + X_lo with
-// X_hi, X_lo exact in f16 (|X| <= 128 * 127) and m, 64 * m exact f16, so one
-// v_mfma_f32_16x16x32_f16 per 16 groups computes it with exact products.
-// Other formats (group 32, per-32 activation scales) fold both terms on the
-// VALU in the GEMV's order.  Tiles are assigned XCD by XCD so that the
-// workgroups sharing a weight tile share one L2.
+// Folding the exact group sums into fp32 is VALU work per output element per
+// group, as much issue time as the MFMAs themselves.  The per-token group-128
+// format keeps it at two instructions, acc = fma(s, float(A), acc), and
+// computes the min term sum_g m * X up front on the f16 MFMA: X = 64 * X_hi +
+// X_lo with 64 * X_hi and X_lo exact in f16 (|X| <= 128 * 127), so each
+// product with the f16 m is exact.  Other formats (group 32, per-32 activation
+// scales) fold both terms on the VALU in the GEMV's order, bit for bit.  Tiles
+// are assigned XCD by XCD so that the workgroups sharing a weight tile share
+// one L2.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -33,21 +35,14 @@
 namespace wq {
 namespace {
 
-constexpr int kBK = 128;       // codes per K step
-constexpr int kBM = 128;       // tokens per tile
-constexpr int kConsumers = 8;  // waves running MFMAs (2 along M x 4 along N)
-constexpr int kProducers = 4;  // waves staging tiles global -> LDS
-constexpr int kThreads = 64 * (kConsumers + kProducers);
-constexpr int kProdThreads = 64 * kProducers;
-constexpr int kXcds = 8;       // MI355X: 8 XCDs, workgroups dispatched round robin
-#ifndef WQ_GEMM_PREFETCH
-#define WQ_GEMM_PREFETCH 4
-#endif
-// K steps of tiles in flight in the producers' registers (even, so that the
-// LDS buffer of an unrolled step is a constant)
-constexpr int kPrefetchSteps = WQ_GEMM_PREFETCH;
+constexpr int kBK = 128;          // codes per K step (= bytes per int8 tile row)
+constexpr int kBM = 128;          // tokens per tile
+constexpr int kWaveGroup = 256;   // 4 waves: 2 along M x 2 along N
+constexpr int kXcds = 8;          // MI355X: 8 XCDs, workgroups dispatched round robin
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 struct GemmParams {
     LinearArgs a;
@@ -55,35 +50,104 @@ struct GemmParams {
     int NE, NG;
 };
 
-template <int BN, int G, bool PT, int MODE, bool DUMP>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
-    constexpr int PF = kPrefetchSteps;
-    constexpr int BM = kBM;
-    constexpr int GE = PT ? G : 32;         // accumulation group
-    constexpr int KS = GE >= 64 ? 64 : 32;  // codes per MFMA
-    constexpr int MPG = GE / KS;            // MFMAs per group and subtile
-    constexpr int NES = kBK / GE;           // accumulation groups per K step
-    constexpr int NGS = kBK / G;            // weight groups per K step
-    constexpr bool FAST = PT && G == 128;   // min term on the f16 MFMA
-    constexpr int WM = BM / 2, WN = BN / 4;
-    constexpr int TM = WM / 16, TN = WN / 16;
-    constexpr int ASTR = kBK + 16;          // LDS row strides (bank spread)
-    constexpr int BSTR = kBK / 2 + 8;
-    constexpr int A_CH = BM * (kBK / 16), B_CH = BN * (kBK / 32);  // 16-byte chunks per tile
-    constexpr int A_PER_T = (A_CH + kProdThreads - 1) / kProdThreads;
-    constexpr int B_PER_T = (B_CH + kProdThreads - 1) / kProdThreads;
-    constexpr int S_PER_T = (BN * NGS + kProdThreads - 1) / kProdThreads;
-    constexpr int X_PER_T = FAST ? 0 : (BM * NES + kProdThreads - 1) / kProdThreads;
-    constexpr int XR = X_PER_T > 0 ? X_PER_T : 1;
-    static_assert(TN >= 1 && BN % 64 == 0, "tile width");
-    static_assert(MODE != 2 || TN % 2 == 0, "mode 2 pairs gate/up subtiles");
-    static_assert(PF % 2 == 0, "even ring: the LDS buffer of an unrolled step is static");
+// Chunk swizzles: activation rows are 128 bytes (8 chunks), packed weight
+// rows 64 bytes (4 chunks); chunk c of row r sits at position c ^ f(r).
+__device__ __forceinline__ int swz_a(int r) { return (r ^ (r >> 3)) & 7; }
+__device__ __forceinline__ int swz_b(int r) { return (r >> 1) & 3; }
 
-    __shared__ __align__(16) unsigned char As[2][BM * ASTR];
-    __shared__ __align__(16) unsigned char Bs[2][BN * BSTR];
-    __shared__ uint32_t Ss[2][BN * NGS];
-    __shared__ __align__(16) float Xs[2][FAST ? 1 : BM * NES];
-    __shared__ __align__(16) float Ds[2][PT ? 1 : BM * NES];
+// 16 codes (8 packed bytes) -> 16 int8 in code order: the low nibbles of a
+// word are codes 8i..8i+3, the high nibbles 8i+4..8i+7.
+__device__ __forceinline__ v4i expand8(uint32_t w0, uint32_t w1) {
+    return v4i{(int)(w0 & kNibbleMask), (int)((w0 >> 4) & kNibbleMask),
+               (int)(w1 & kNibbleMask), (int)((w1 >> 4) & kNibbleMask)};
+}
+
+// End of a pipeline step: wait until at most n vector-memory operations of
+// this wave are in flight and all its LDS operations are done, then barrier.
+// The barrier carries no memory fence, so loads issued for later steps stay
+// in flight across it.
+template <int n>
+__device__ __forceinline__ void step_barrier() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4));
+    asm volatile("s_barrier" ::: "memory");
+}
+
+// Direct global -> LDS loads of 16 (4) bytes per lane: lane l's bytes land at
+// LDS address lds + 16 l (4 l); base and lds are wave-uniform, off per lane.
+// Written as inline assembly so that the compiler's wait-count pass does not
+// track them: it cannot tell the stages of the ring apart and would wait for
+// every load in flight before the first LDS read of a step.  The waits these
+// loads need are explicit (step_barrier); for loads the compiler does track,
+// untracked loads issued in between only make its waits stricter.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)p);
+}
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, const void* lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 ::"v"(off), "s"(uniform_ptr(base)), "s"(lds_addr(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, const void* lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+                 ::"v"(off), "s"(uniform_ptr(base)), "s"(lds_addr(lds)) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Threads of a workgroup: the per-token group-128 format runs two groups of
+// 4 waves on alternate K steps (two waves per SIMD, so that one wave's fold
+// overlaps the other's MFMAs), the other formats one group (their fp32 fold
+// order is fixed).
+constexpr int gemm_threads(int G, bool PT) { return PT && G == 128 ? 2 * kWaveGroup : kWaveGroup; }
+
+template <int BN, int G, bool PT, int MODE, bool DUMP>
+__global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p) {
+    constexpr int BM = kBM;
+    constexpr int GE = PT ? G : 32;          // accumulation group
+    constexpr bool FAST = PT && G == 128;    // min term on the f16 MFMA
+    constexpr int KS = FAST ? 2 : 1;         // wave groups splitting the K steps
+    constexpr int NES = kBK / GE;            // accumulation groups per step
+    constexpr int NGS = kBK / G;             // weight groups per step
+    constexpr int TM = 2;                    // 32-token subtiles per wave
+    constexpr int TN = BN / 64;              // 32-row subtiles per wave
+    constexpr int NST = FAST ? 4 : 3;        // LDS stages (steps in flight + 1)
+    // direct-to-LDS instructions per wave and step (4 waves share each tile)
+    constexpr int A_PW = BM * kBK / 1024 / 4;          // 1 KiB activation blocks
+    constexpr int B_PW = BN * (kBK / 2) / 1024 / 4;    // 1 KiB packed weight blocks
+    constexpr int S_W = BN * NGS;                      // scale words per step
+    constexpr int S_PW = (S_W + 255) / 256;            // 64-word blocks
+    constexpr int X_PW = FAST ? 0 : NES * BM / 256;    // group sums (non-fast)
+    constexpr int D_PW = PT ? 0 : NES * BM / 256;      // per-32 scales
+    constexpr int VM = A_PW + B_PW + S_PW + X_PW + D_PW;
+    static_assert(BN % 64 == 0 && B_PW == TN, "tile width");
+    static_assert(MODE != 2 || TN % 2 == 0, "mode 2 pairs gate/up subtiles");
+    static_assert((NST - 2) * VM < 64, "vmcnt range");
+
+    // LDS: NST stages of (activations, packed weights, scale words, group
+    // sums, per-32 scales); the partial sums of the second wave group reuse
+    // it at the end
+    constexpr int A_SZ = BM * kBK, B_SZ = BN * kBK / 2, S_SZ = S_PW * 1024;
+    constexpr int X_SZ = FAST ? 16 : NES * BM * 4, D_SZ = PT ? 16 : NES * BM * 4;
+    constexpr int ST_SZ = A_SZ + B_SZ + S_SZ + X_SZ + D_SZ;
+    constexpr int RED_SZ = KS > 1 ? kWaveGroup * TM * TN * 16 * 4 : 0;
+    constexpr int LDS_SZ = NST * ST_SZ > RED_SZ ? NST * ST_SZ : RED_SZ;
+    __shared__ __align__(1024) unsigned char lds[LDS_SZ];
+    auto As = [&](int st) -> int8_t* { return reinterpret_cast<int8_t*>(lds + st * ST_SZ); };
+    auto Bs = [&](int st) -> uint32_t* { return reinterpret_cast<uint32_t*>(lds + st * ST_SZ + A_SZ); };
+    auto Ss = [&](int st) -> uint32_t* { return reinterpret_cast<uint32_t*>(lds + st * ST_SZ + A_SZ + B_SZ); };
+    auto Xs = [&](int st) -> int32_t* {  // [group][token]
+        return reinterpret_cast<int32_t*>(lds + st * ST_SZ + A_SZ + B_SZ + S_SZ);
+    };
+    auto Ds = [&](int st) -> float* {
+        return reinterpret_cast<float*>(lds + st * ST_SZ + A_SZ + B_SZ + S_SZ + X_SZ);
+    };
 
     const LinearArgs& a = p.a;
     pin_arg(a.wq); pin_arg(a.ws); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs); pin_arg(a.y);
@@ -93,13 +157,17 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // wave group (K steps s with s % KS == wk) and wave within its group;
+    // wave-uniform, so that every step and stage index derived from them
+    // stays scalar
+    const int wk = __builtin_amdgcn_readfirstlane(tid / kWaveGroup);
+    const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);
     const int64_t M = a.M, N = a.N;
     const int K = (int)a.K;
     const int NG = p.NG, NE = p.NE;
     const int nsteps = K / kBK;
 
-    // XCD-aware tile order: consecutive tiles (same weight columns) on one XCD
+    // XCD-aware tile order: consecutive tiles (same weight rows) on one XCD
     const int T = p.tilesM * p.tilesN;
     const int bid = blockIdx.x;
     const int xcd = bid % kXcds, li = bid / kXcds;
@@ -125,323 +193,360 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
         return t < M ? t : M - 1;
     };
 
-    if (wave >= kConsumers) {
-        // ---------------- producer waves: global -> register ring -> LDS ----
-        const int pt = tid - 64 * kConsumers;
-        const unsigned char* xq_b = reinterpret_cast<const unsigned char*>(a.xq);
-        const unsigned char* wq_b = reinterpret_cast<const unsigned char*>(a.wq);
-        uint32_t a_off[A_PER_T], b_off[B_PER_T], s_off[S_PER_T], x_off[XR], d_off[XR];
-        int a_dst[A_PER_T], b_dst[B_PER_T];
+    // ---------------- staging: per-lane source offsets ----------------
+    // A direct-to-LDS instruction writes 64 consecutive 16-byte (or 4-byte)
+    // slots, lane l the l-th; each lane fetches whatever belongs in its slot.
+    uint32_t a_off[A_PW], b_off[B_PW], s_off[S_PW], x_off[X_PW > 0 ? X_PW : 1], d_off[D_PW > 0 ? D_PW : 1];
 #pragma unroll
-        for (int i = 0; i < A_PER_T; ++i) {
-            int c = pt + kProdThreads * i;
-            c = c < A_CH ? c : A_CH - 1;
-            int r = c / (kBK / 16), c16 = c % (kBK / 16);
-            a_off[i] = (uint32_t)(trow(r) * K + 16 * c16);
-            a_dst[i] = r * ASTR + 16 * c16;
-        }
-#pragma unroll
-        for (int i = 0; i < B_PER_T; ++i) {
-            int c = pt + kProdThreads * i;
-            c = c < B_CH ? c : B_CH - 1;
-            int r = c / (kBK / 32), c16 = c % (kBK / 32);
-            b_off[i] = (uint32_t)(wrow(r) * (K / 2) + 16 * c16);
-            b_dst[i] = r * BSTR + 16 * c16;
-        }
-#pragma unroll
-        for (int i = 0; i < S_PER_T; ++i) {
-            int c = pt + kProdThreads * i;
-            c = c < BN * NGS ? c : 0;
-            s_off[i] = (uint32_t)(wrow(c / NGS) * NG + c % NGS);
-        }
-#pragma unroll
-        for (int i = 0; i < X_PER_T; ++i) {
-            int c = pt + kProdThreads * i;
-            c = c < BM * NES ? c : 0;
-            x_off[i] = (uint32_t)(trow(c / NES) * NE + c % NES);
-            d_off[i] = (uint32_t)(trow(c / NES) * (K / 32) + c % NES);
-        }
-        // ring of PF steps in flight; every load is unconditional (steps past
-        // the end re-read the last one) so the wait before a stage covers only
-        // the oldest slot
-        uint4 ra[PF][A_PER_T], rb[PF][B_PER_T];
-        uint32_t rs[PF][S_PER_T];
-        int32_t rx[PF][XR];
-        float rd[PF][XR];
-        auto prefetch = [&](int step, const int q) {
-            step = step < nsteps ? step : nsteps - 1;
-            const int k0 = step * kBK;
-#pragma unroll
-            for (int i = 0; i < A_PER_T; ++i) ra[q][i] = load16(xq_b + a_off[i] + k0);
-#pragma unroll
-            for (int i = 0; i < B_PER_T; ++i) rb[q][i] = load_stream16(wq_b + b_off[i] + k0 / 2);
-#pragma unroll
-            for (int i = 0; i < S_PER_T; ++i) rs[q][i] = a.ws[s_off[i] + step * NGS];
-#pragma unroll
-            for (int i = 0; i < X_PER_T; ++i) {
-                rx[q][i] = a.xs[x_off[i] + step * NES];
-                if (!PT) rd[q][i] = a.dx[d_off[i] + step * NES];
-            }
-        };
-        auto stage = [&](const int buf, const int q) {
-#pragma unroll
-            for (int i = 0; i < A_PER_T; ++i)
-                if (A_CH % kProdThreads == 0 || pt + kProdThreads * i < A_CH)
-                    *reinterpret_cast<uint4*>(&As[buf][a_dst[i]]) = ra[q][i];
-#pragma unroll
-            for (int i = 0; i < B_PER_T; ++i) {
-                if (B_CH % kProdThreads == 0 || pt + kProdThreads * i < B_CH) {
-                    uint2* dst = reinterpret_cast<uint2*>(&Bs[buf][b_dst[i]]);
-                    dst[0] = make_uint2(rb[q][i].x, rb[q][i].y);
-                    dst[1] = make_uint2(rb[q][i].z, rb[q][i].w);
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < S_PER_T; ++i) {
-                int c = pt + kProdThreads * i;
-                if (c < BN * NGS) Ss[buf][c] = rs[q][i];
-            }
-#pragma unroll
-            for (int i = 0; i < X_PER_T; ++i) {
-                int c = pt + kProdThreads * i;
-                if (c < BM * NES) {
-                    Xs[buf][c] = (float)rx[q][i];
-                    if (!PT) Ds[buf][c] = rd[q][i];
-                }
-            }
-        };
-#pragma unroll
-        for (int q = 0; q < PF; ++q) prefetch(q, q);
-        stage(0, 0);
-        prefetch(PF, 0);  // slot s % PF holds step s: slot 0 moves on to step PF
-        __syncthreads();
-        // iteration i: stage step i + 1 (slot (i+1) % PF) into the buffer the
-        // consumers are not reading, refill that slot with step i + 1 + PF
-        for (int s0 = 0; s0 < nsteps; s0 += PF) {
-#pragma unroll
-            for (int u = 0; u < PF; ++u) {
-                stage((u + 1) & 1, (u + 1) % PF);
-                prefetch(s0 + u + 1 + PF, (u + 1) % PF);
-                if (s0 + u < nsteps) __syncthreads();
-            }
-        }
-        return;
+    for (int i = 0; i < A_PW; ++i) {  // block = 8 rows of 128 B
+        const int r = 8 * (A_PW * wave + i) + lane / 8;
+        a_off[i] = (uint32_t)(trow(r) * K + 16 * ((lane % 8) ^ swz_a(r)));
     }
-
-    // ---------------- consumer waves (2 along M x 4 along N) ----------------
-    const int wm = wave >> 2, wn = wave & 3;
-    const int l16 = lane & 15, lq = lane >> 4;
-    // tile row (of W) of this lane's column in subtile jj
-    auto bcol = [&](int jj) -> int {
-        if (MODE == 2) {
-            constexpr int H = TN / 2;
-            return (jj < H ? wn * (BN / 8) + 16 * jj : BN / 2 + wn * (BN / 8) + 16 * (jj - H)) + l16;
+#pragma unroll
+    for (int i = 0; i < B_PW; ++i) {  // block = 16 rows of 64 B
+        const int r = 16 * (B_PW * wave + i) + lane / 4;
+        b_off[i] = (uint32_t)(wrow(r) * (K / 2) + 16 * ((lane % 4) ^ swz_b(r)));
+    }
+#pragma unroll
+    for (int i = 0; i < S_PW; ++i) {  // block = 64 scale words, [row][group]
+        int w = 64 * (S_PW * wave + i) + lane;
+        w = w < S_W ? w : 0;  // padding slots re-read word 0
+        s_off[i] = (uint32_t)(wrow(w / NGS) * NG + w % NGS);
+    }
+#pragma unroll
+    for (int i = 0; i < X_PW; ++i) {  // block = 64 tokens of one group, [group][token]
+        const int w = 64 * (X_PW * wave + i) + lane;
+        x_off[i] = (uint32_t)(trow(w % BM) * NE + w / BM);
+    }
+#pragma unroll
+    for (int i = 0; i < D_PW; ++i) {
+        const int w = 64 * (D_PW * wave + i) + lane;
+        d_off[i] = (uint32_t)(trow(w % BM) * (K / 32) + w / BM);
+    }
+    // Every load is unconditional (steps past the end re-read the last one),
+    // so each call issues exactly VM vector-memory instructions per wave.
+    auto dma = [&](int step, const int st) {
+        step = step < nsteps ? step : nsteps - 1;
+        const int8_t* xq = a.xq + step * kBK;
+        const uint8_t* wq = reinterpret_cast<const uint8_t*>(a.wq) + step * (kBK / 2);
+        const uint32_t* ws = a.ws + step * NGS;
+#pragma unroll
+        for (int i = 0; i < A_PW; ++i) dma16(xq, a_off[i], As(st) + 1024 * (A_PW * wave + i));
+#pragma unroll
+        for (int i = 0; i < B_PW; ++i) dma16(wq, b_off[i], Bs(st) + 256 * (B_PW * wave + i));
+#pragma unroll
+        for (int i = 0; i < S_PW; ++i) dma4(ws, 4 * s_off[i], Ss(st) + 64 * (S_PW * wave + i));
+        if constexpr (!FAST) {
+            const int32_t* xs = a.xs + step * NES;
+#pragma unroll
+            for (int i = 0; i < X_PW; ++i) dma4(xs, 4 * x_off[i], Xs(st) + 64 * (X_PW * wave + i));
         }
-        return wn * WN + 16 * jj + l16;
+        if constexpr (!PT) {
+            const float* dxp = a.dx + step * NES;
+#pragma unroll
+            for (int i = 0; i < D_PW; ++i) dma4(dxp, 4 * d_off[i], Ds(st) + 64 * (D_PW * wave + i));
+        }
     };
 
-    v4f facc[TM][TN];
+    // prologue loads: one group loads steps 0 .. NST-2; two groups load
+    // their first step each
+    if (KS == 1) {
+#pragma unroll
+        for (int q = 0; q < NST - 1; ++q) dma(q, q);
+    } else {
+        dma(wk, wk);
+    }
+
+    // ---------------- compute layout ----------------
+    const int wm = wave >> 1, wn = wave & 1;
+    const int l32 = lane & 31, h = lane >> 5;
+    // tile row (of W) of this lane's column in subtile j
+    auto bcol = [&](int j) -> int {
+        if (MODE == 2) {
+            constexpr int H = TN / 2;
+            return (j < H ? wn * (BN / 4) + 32 * j : BN / 2 + wn * (BN / 4) + 32 * (j - H)) + l32;
+        }
+        return wn * (BN / 2) + 32 * j + l32;
+    };
+    // token row (within the tile) of accumulator element r of subtile i
+    auto arow = [&](int i, int r) -> int { return wm * 64 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3); };
+
+    v16f facc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int jj = 0; jj < TN; ++jj) facc[i][jj] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TN; ++j) facc[i][j] = v16f{};
 
-    if (FAST) {
-        // min term: facc = sum_g m[n,g] * X[t,g] on v_mfma_f32_16x16x32_f16.
-        // Lane quarter lq holds k = 8 lq .. 8 lq + 7 of both operands:
-        // lq 0/1 -> (X_hi, 64 m) of groups 0-7 / 8-15, lq 2/3 -> (X_lo, m).
-        // All loads of a block are issued before any is used (indices past
-        // the last group are clamped, their values zeroed afterwards).
-        const int gq = 8 * (lq & 1);
-        const bool hi_half = lq < 2;
-        for (int b = 0; b < NG; b += 16) {
+    // min term: facc += sum_g m[n,g] * X[t,g] (per-token group-128 format
+    // only) on v_mfma_f32_32x32x16_f16.  One MFMA covers 8 groups: lane half
+    // h = 0 holds (64 X_hi, m), h = 1 (X_lo, m) of groups b .. b+7, both
+    // halves of a row reading the same 32 bytes.
+    auto min_term_block = [&](const int32_t (&xv)[TM][8], const uint32_t (&wv)[TN][8], int b) {
+        v8h xa[TM], mb[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int32_t v = b + u < NG ? xv[i][u] : 0;
+                xa[i][u] = (_Float16)(h == 0 ? (float)((v >> 6) * 64) : (float)(v & 63));
+            }
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                mb[j][u] = b + u < NG ? __builtin_bit_cast(_Float16, (unsigned short)(wv[j][u] >> 16))
+                                      : (_Float16)0.0f;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                facc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[i], mb[j], facc[i][j], 0, 0, 0);
+    };
+    auto min_term = [&]() {
+        const int32_t* xr[TM];
+        const uint32_t* sr[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) xr[i] = a.xs + trow(wm * 64 + 32 * i + l32) * NE;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) sr[j] = a.ws + wrow(bcol(j)) * NG;
+        // full blocks: rows are 32-byte aligned when the group count is a
+        // multiple of 8 (K a multiple of 1024)
+        const int nfull = NG % 8 == 0 ? NG / 8 : 0;
+        for (int blk = 0; blk < nfull; ++blk) {
             int32_t xv[TM][8];
             uint32_t wv[TN][8];
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
-                const int32_t* xr = a.xs + trow(wm * WM + 16 * i + l16) * NE;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int g = b + gq + u;
-                    xv[i][u] = xr[g < NG ? g : NG - 1];
-                }
+                const int4 lo = *reinterpret_cast<const int4*>(xr[i] + 8 * blk);
+                const int4 hi = *reinterpret_cast<const int4*>(xr[i] + 8 * blk + 4);
+                xv[i][0] = lo.x; xv[i][1] = lo.y; xv[i][2] = lo.z; xv[i][3] = lo.w;
+                xv[i][4] = hi.x; xv[i][5] = hi.y; xv[i][6] = hi.z; xv[i][7] = hi.w;
             }
 #pragma unroll
-            for (int jj = 0; jj < TN; ++jj) {
-                const uint32_t* sr = a.ws + wrow(bcol(jj)) * NG;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int g = b + gq + u;
-                    wv[jj][u] = sr[g < NG ? g : NG - 1];
-                }
+            for (int j = 0; j < TN; ++j) {
+                const uint4 lo = *reinterpret_cast<const uint4*>(sr[j] + 8 * blk);
+                const uint4 hi = *reinterpret_cast<const uint4*>(sr[j] + 8 * blk + 4);
+                wv[j][0] = lo.x; wv[j][1] = lo.y; wv[j][2] = lo.z; wv[j][3] = lo.w;
+                wv[j][4] = hi.x; wv[j][5] = hi.y; wv[j][6] = hi.z; wv[j][7] = hi.w;
             }
-            v8h xa[TM], mb[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int32_t v = b + gq + u < NG ? xv[i][u] : 0;
-                    xa[i][u] = (_Float16)(hi_half ? (v >> 6) : (v & 63));
-                }
-#pragma unroll
-            for (int jj = 0; jj < TN; ++jj)
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const float m = b + gq + u < NG ? f16hi(wv[jj][u]) : 0.0f;
-                    mb[jj][u] = (_Float16)(hi_half ? 64.0f * m : m);
-                }
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int jj = 0; jj < TN; ++jj)
-                    facc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[i], mb[jj], facc[i][jj], 0, 0, 0);
+            min_term_block(xv, wv, 8 * blk);
         }
-    }
-    // per-token scales of this lane's 16 output rows, fetched early
-    float dtok[TM][4];
+        // otherwise word by word, indices past the last group clamped and
+        // their values zeroed
+        for (int b = 8 * nfull; b < NG; b += 8) {
+            int32_t xv[TM][8];
+            uint32_t wv[TN][8];
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dtok[i][r] = PT ? a.dx[trow(wm * WM + 16 * i + 4 * lq + r)] : 1.0f;
-    const int rows_total = MODE == 2 ? 2 * (int)N : (int)N;
-    __syncthreads();  // step 0 is staged
+                for (int u = 0; u < 8; ++u) xv[i][u] = xr[i][b + u < NG ? b + u : NG - 1];
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int u = 0; u < 8; ++u) wv[j][u] = sr[j][b + u < NG ? b + u : NG - 1];
+            min_term_block(xv, wv, b);
+        }
+    };
+    // the min term is added once, by wave group 0
+    if (FAST && wk == 0) min_term();
 
-    auto compute = [&](const int step, const int buf) {
-        const unsigned char* Ab = As[buf];
-        const unsigned char* Bb = Bs[buf];
-#pragma unroll 1
-        for (int ge = 0; ge < NES; ++ge) {
-            // activation sums / scales of this lane's 4 tokens per subtile row
-            float xg[TM][4], dg[TM][4];
-            if (!FAST) {
+    // the first step of each group has landed
+    step_barrier<KS == 1 ? (NST - 2) * VM : 0>();
+
+    const int rows_total = MODE == 2 ? 2 * (int)N : (int)N;
+    auto dump = [&](int step, int e_local, int i, int br, const v16i& acc) {
+        const int64_t e = (int64_t)step * NES + e_local;
+        const int64_t nn = n0 + (MODE == 2 ? (br < BN / 2 ? br : br - BN / 2) : br);
+        const int64_t wr = MODE == 2 && br >= BN / 2 ? nn + N : nn;
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
+        for (int r = 0; r < 16; ++r) {
+            const int64_t t = m0 + arow(i, r);
+            if (t < M && nn < N) a.acc_dump[(t * rows_total + wr) * NE + e] = acc[r];
+        }
+    };
+
+    auto compute = [&](const int step, const int st) {
+        const int8_t* Ab = As(st);
+        const uint8_t* Bb = reinterpret_cast<const uint8_t*>(Bs(st));
+        const uint32_t* Sb = Ss(st);
+        if (FAST) {
+            // k-slice ks of lane half h = codes 64 h + 16 ks .. +15 of the
+            // group (any assignment shared by both operands gives the same
+            // sums): 32 contiguous packed bytes per lane and weight row
+            v4i af[4][TM];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int tr = wm * WM + 16 * i + 4 * lq + r;
-                        xg[i][r] = Xs[buf][tr * NES + ge];
-                        dg[i][r] = PT ? 0.0f : Ds[buf][tr * NES + ge];
-                    }
+            for (int i = 0; i < TM; ++i) {
+                const int ra = wm * 64 + 32 * i + l32;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks)
+                    af[ks][i] = *reinterpret_cast<const v4i*>(Ab + ra * kBK + 16 * ((4 * h + ks) ^ swz_a(ra)));
             }
-            // A fragments of the whole group (MPG k-slices)
-            v4i af4[MPG][TM];
-            long af2[MPG][TM];
 #pragma unroll
-            for (int kk = 0; kk < MPG; ++kk) {
-                const int koff = ge * GE + kk * KS;
+            for (int j = 0; j < TN; ++j) {
+                const int br = bcol(j);
+                const uint4 p0 = *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * ((2 * h) ^ swz_b(br)));
+                const uint4 p1 = *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * ((2 * h + 1) ^ swz_b(br)));
+                const v4i bf[4] = {expand8(p0.x, p0.y), expand8(p0.z, p0.w), expand8(p1.x, p1.y),
+                                   expand8(p1.z, p1.w)};
+                v16i acc[TM];
 #pragma unroll
-                for (int i = 0; i < TM; ++i) {
-                    const int r = wm * WM + 16 * i + l16;
-                    if (KS == 64)
-                        af4[kk][i] = *reinterpret_cast<const v4i*>(Ab + r * ASTR + koff + 16 * lq);
-                    else
-                        af2[kk][i] = *reinterpret_cast<const long*>(Ab + r * ASTR + koff + 8 * lq);
-                }
-            }
-#pragma unroll
-            for (int jj = 0; jj < TN; ++jj) {
-                const int br = bcol(jj);
-                v4i iacc[TM];
-#pragma unroll
-                for (int kk = 0; kk < MPG; ++kk) {
-                    const int koff = ge * GE + kk * KS;
-                    if (KS == 64) {
-                        uint2 w = *reinterpret_cast<const uint2*>(Bb + br * BSTR + koff / 2 + 8 * lq);
-                        v4i bf = v4i{(int)(w.x & kNibbleMask), (int)((w.x >> 4) & kNibbleMask),
-                                     (int)(w.y & kNibbleMask), (int)((w.y >> 4) & kNibbleMask)};
-#pragma unroll
-                        for (int i = 0; i < TM; ++i)
-                            iacc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                                af4[kk][i], bf, kk == 0 ? v4i{0, 0, 0, 0} : iacc[i], 0, 0, 0);
-                    } else {
-                        uint32_t w = *reinterpret_cast<const uint32_t*>(Bb + br * BSTR + koff / 2 + 4 * lq);
-                        long bf = (long)((uint64_t)(w & kNibbleMask) | ((uint64_t)((w >> 4) & kNibbleMask) << 32));
-#pragma unroll
-                        for (int i = 0; i < TM; ++i)
-                            iacc[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                                af2[kk][i], bf, kk == 0 ? v4i{0, 0, 0, 0} : iacc[i], 0, 0, 0);
-                    }
-                }
-                if (DUMP) {  // test hook: the exact group sums this tile produced
-                    const int64_t e = (int64_t)step * NES + ge;
-                    const int64_t nn = n0 + (MODE == 2 ? (br < BN / 2 ? br : br - BN / 2) : br);
-                    const int64_t wr = MODE == 2 && br >= BN / 2 ? nn + N : nn;
+                for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
                     for (int i = 0; i < TM; ++i)
+                        acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks], ks == 0 ? v16i{} : acc[i],
+                                                                       0, 0, 0);
+                const float s = f16lo(Sb[br]);
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const int64_t t = m0 + wm * WM + 16 * i + 4 * lq + r;
-                            if (t < M && nn < N) a.acc_dump[(t * rows_total + wr) * NE + e] = iacc[i][r];
-                        }
+                for (int i = 0; i < TM; ++i) {
+                    if (DUMP) dump(step, 0, i, br, acc[i]);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) facc[i][j][r] = fmaf(s, (float)acc[i][r], facc[i][j][r]);
                 }
-                // fold the exact group sums into the fp32 accumulators
-                const uint32_t sw = Ss[buf][br * NGS + (ge * GE) / G];
-                const float s = f16lo(sw), m = f16hi(sw);
+            }
+        } else {
+            // one MFMA per accumulation group of 32 codes, groups in order;
+            // lane half h takes codes 32 ks + 16 h .. +15
+#pragma unroll 1
+            for (int ks = 0; ks < 4; ++ks) {
+                v4i af[TM];
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
+                for (int i = 0; i < TM; ++i) {
+                    const int ra = wm * 64 + 32 * i + l32;
+                    af[i] = *reinterpret_cast<const v4i*>(Ab + ra * kBK + 16 * ((2 * ks + h) ^ swz_a(ra)));
+                }
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        float v = facc[i][jj][r];
-                        if (FAST) {
-                            v = fmaf(s, (float)iacc[i][r], v);
-                        } else if (PT) {
-                            v = fmaf(s, (float)iacc[i][r], v);
-                            v = fmaf(m, xg[i][r], v);
-                        } else {
-                            v = fmaf(s * dg[i][r], (float)iacc[i][r], v);
-                            v = fmaf(m * dg[i][r], xg[i][r], v);
+                for (int j = 0; j < TN; ++j) {
+                    const int br = bcol(j);
+                    const uint2 pw = *reinterpret_cast<const uint2*>(Bb + br * 64 + 16 * (ks ^ swz_b(br)) + 8 * h);
+                    const v4i bf = expand8(pw.x, pw.y);
+                    const uint32_t sw = Sb[br * NGS + (32 * ks) / G];
+                    const float s = f16lo(sw), m = f16hi(sw);
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+                        const v16i acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf, v16i{}, 0, 0, 0);
+                        if (DUMP) dump(step, ks, i, br, acc);
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const int tr = wm * 64 + 32 * i + 8 * q + 4 * h;
+                            const int4 xg = *reinterpret_cast<const int4*>(&Xs(st)[ks * BM + tr]);
+                            float4 dg = make_float4(0.f, 0.f, 0.f, 0.f);
+                            if (!PT) dg = *reinterpret_cast<const float4*>(&Ds(st)[ks * BM + tr]);
+                            const float xr[4] = {(float)xg.x, (float)xg.y, (float)xg.z, (float)xg.w};
+                            const float dr[4] = {dg.x, dg.y, dg.z, dg.w};
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) {
+                                const int r = 4 * q + u;
+                                float v = facc[i][j][r];
+                                if (PT) {
+                                    v = fmaf(s, (float)acc[r], v);
+                                    v = fmaf(m, xr[u], v);
+                                } else {
+                                    v = fmaf(s * dr[u], (float)acc[r], v);
+                                    v = fmaf(m * dr[u], xr[u], v);
+                                }
+                                facc[i][j][r] = v;
+                            }
                         }
-                        facc[i][jj][r] = v;
                     }
+                }
             }
         }
     };
-    for (int s0 = 0; s0 < nsteps; s0 += PF) {
-#pragma unroll
-        for (int u = 0; u < PF; ++u) {
-            if (s0 + u < nsteps) {
-                compute(s0 + u, u & 1);
-                __syncthreads();
-            }
+
+    if (KS == 1) {
+        // step s: load step s + NST - 1 into stage (s - 1) % NST, which step
+        // s - 1 left before the last barrier; compute step s from stage
+        // s % NST; wait for the loads of step s + 1 and barrier.
+        for (int s = 0; s < nsteps; ++s) {
+            dma(s + NST - 1, (s + NST - 1) % NST);
+            compute(s, s % NST);
+            step_barrier<(NST - 2) * VM>();
         }
+    } else {
+        // round r: group wk loads step 2r + 2 + wk into the stage that its
+        // step 2r - 2 + wk left and computes step 2r + wk; both steps of the
+        // next round land before the barrier.
+        for (int r = 0; KS * r < nsteps; ++r) {
+            const int sl = KS * r + KS + wk, sc = KS * r + wk;
+            dma(sl, sl % NST);
+            if (sc < nsteps) compute(sc, sc % NST);
+            step_barrier<0>();
+        }
+    }
+    // no direct-to-LDS load may outlive the workgroup
+    step_barrier<0>();
+
+    // subtiles this wave stores: all of them with one wave group; with two,
+    // group g stores subtile row i = g after adding the other group's partial
+    // sums (exchanged through LDS, lane-major; the fp32 addition of two
+    // partials is the same in either order)
+    constexpr int I0 = 0, I1 = KS > 1 ? 1 : TM;
+    int ilo = I0, ihi = I1;
+    if constexpr (KS > 1) {
+        static_assert(TM == 2, "one subtile row per wave group");
+        float* red = reinterpret_cast<float*>(lds);
+        const int give = 1 - wk;  // the subtile row the other group stores
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                red[(((give * 4 + wave) * TN + j) * 16 + r) * 64 + lane] = wk == 0 ? facc[1][j][r] : facc[0][j][r];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float o = red[(((wk * 4 + wave) * TN + j) * 16 + r) * 64 + lane];
+                if (wk == 0) facc[0][j][r] = facc[0][j][r] + o;
+                else facc[1][j][r] = o + facc[1][j][r];
+            }
+        ilo = wk;
+        ihi = wk + 1;
     }
 
     // epilogue: per-token scale, output mode, store (mode 1 reads every old
     // value of its outputs in one batch first)
     constexpr int JO = MODE == 2 ? TN / 2 : TN;
-    float yold[MODE == 1 ? TM : 1][4][MODE == 1 ? JO : 1];
+    float dtok[TM][16];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            dtok[i][r] = PT && i >= ilo && i < ihi ? a.dx[trow(arow(i, r))] : 1.0f;
+    float yold[MODE == 1 ? TM : 1][MODE == 1 ? JO : 1][16];
     if (MODE == 1) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i) {
+            if (i < ilo || i >= ihi) continue;
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
+            for (int j = 0; j < JO; ++j) {
+                int64_t n = n0 + bcol(j);
+                n = n < N ? n : N - 1;
 #pragma unroll
-                for (int jj = 0; jj < JO; ++jj) {
-                    const int64_t t = trow(wm * WM + 16 * i + 4 * lq + r);
-                    int64_t n = n0 + bcol(jj);
-                    n = n < N ? n : N - 1;
-                    yold[i][r][jj] = a.y[t * N + n];
-                }
+                for (int r = 0; r < 16; ++r) yold[i][j][r] = a.y[trow(arow(i, r)) * N + n];
+            }
+        }
     }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
+        if (i < ilo || i >= ihi) continue;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t t = m0 + wm * WM + 16 * i + 4 * lq + r;
+        for (int r = 0; r < 16; ++r) {
+            const int64_t t = m0 + arow(i, r);
             if (t >= M) continue;
             const float d = dtok[i][r];
 #pragma unroll
-            for (int jj = 0; jj < JO; ++jj) {
-                const int64_t n = n0 + bcol(jj);
+            for (int j = 0; j < JO; ++j) {
+                const int64_t n = n0 + bcol(j);
                 if (n >= N) continue;
-                float v = PT ? facc[i][jj][r] * d : facc[i][jj][r];
+                const float v = PT ? facc[i][j][r] * d : facc[i][j][r];
                 float* yo = a.y + t * N + n;
                 if (MODE == 0) {
                     *yo = v;
                 } else if (MODE == 1) {
-                    *yo = yold[i][r][jj] + v;
+                    *yo = yold[i][j][r] + v;
                 } else {
-                    float u = PT ? facc[i][jj + TN / 2][r] * d : facc[i][jj + TN / 2][r];
+                    const float u = PT ? facc[i][j + TN / 2][r] * d : facc[i][j + TN / 2][r];
                     *yo = silu_mul(v, u);
                 }
             }
@@ -451,7 +556,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
 
 template <int BN, int G, bool PT, bool DUMP>
 hipError_t launch_mode(const GemmParams& gp, hipStream_t s) {
-    dim3 grid((unsigned)(gp.tilesM * gp.tilesN)), block(kThreads);
+    dim3 grid((unsigned)(gp.tilesM * gp.tilesN)), block(gemm_threads(G, PT));
     switch (gp.a.mode) {
         case 0: hipLaunchKernelGGL((gemm_kernel<BN, G, PT, 0, DUMP>), grid, block, 0, s, gp); break;
         case 1: hipLaunchKernelGGL((gemm_kernel<BN, G, PT, 1, DUMP>), grid, block, 0, s, gp); break;
@@ -487,26 +592,28 @@ hipError_t launch_tile(const LinearArgs& a, hipStream_t s) {
 int pick_bn(const LinearArgs& a) {
     const int64_t tm = (a.M + kBM - 1) / kBM;
     if (a.mode == 2) return tm * ((a.N + 127) / 128) >= 256 ? 256 : 128;
-    static const int choices[] = {192, 128, 64};
+    static const int choices[] = {256, 192, 128, 64};
     for (int bn : choices)
         if (tm * ((a.N + bn - 1) / bn) >= 256) return bn;
     return 64;
 }
 
-template <bool DUMP>
 hipError_t launch_bn(const LinearArgs& a, hipStream_t s) {
     switch (pick_bn(a)) {
-        case 256: return launch_tile<256, DUMP>(a, s);
-        case 192: return launch_tile<192, DUMP>(a, s);
-        case 128: return launch_tile<128, DUMP>(a, s);
-        default: return launch_tile<64, DUMP>(a, s);
+        case 256: return launch_tile<256, false>(a, s);
+        case 192: return launch_tile<192, false>(a, s);
+        case 128: return launch_tile<128, false>(a, s);
+        default: return launch_tile<64, false>(a, s);
     }
 }
 
 }  // namespace
 
+// The group-sum dump (a test hook) runs the narrowest tiles: same kernels and
+// operand paths, fewer registers for the extra stores.
 hipError_t launch_gemm(const LinearArgs& a, hipStream_t s) {
-    return a.acc_dump ? launch_bn<true>(a, s) : launch_bn<false>(a, s);
+    if (a.acc_dump) return a.mode == 2 ? launch_tile<128, true>(a, s) : launch_tile<64, true>(a, s);
+    return launch_bn(a, s);
 }
 
 }  // namespace wq
