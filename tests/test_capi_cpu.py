@@ -58,8 +58,11 @@ def test_linear_argument_errors(fn):
 def test_gemv_token_and_k_limits():
     assert gemv(M=9) == _lib.WQ_ESHAPE and "M = 9" in err()
     assert gemv(K=2048 * 9) == _lib.WQ_ESHAPE
-    # the GEMM takes any M (and the same K)
+    # the GEMM takes any M (and the same K) ...
     assert gemv(M=9, mode=7, fn="wq_gemm") == _lib.WQ_EINVAL
+    # ... while each operand stays within 4 GiB of 32-bit staging offsets
+    assert gemv(M=1 << 20, K=8192, fn="wq_gemm") == _lib.WQ_ESHAPE and "4 GiB" in err()
+    assert gemv(N=1 << 20, K=8192, mode=2, fn="wq_gemm") == _lib.WQ_ESHAPE
 
 
 def test_matmul_paths():

@@ -136,6 +136,12 @@ int gemm_impl(const char* fn, void* stream, const uint32_t* wq, const uint32_t* 
               int64_t M, int32_t GA, int32_t mode, float* y, int32_t* acc) {
     int rc = check_linear(fn, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, true);
     if (rc) return rc;
+    // the GEMM stages tiles with 32-bit byte offsets from each operand's base
+    const int64_t rows = mode == WQ_MODE_SILU_MUL ? 2 * N : N;
+    const int64_t lim = int64_t(0xFFFFFFFF);
+    if (M * K > lim || rows * (K / 2) > lim)
+        return fail(WQ_ESHAPE, "%s: M = %lld, rows = %lld, K = %lld address more than 4 GiB of one operand; "
+                    "split the call along M or N", fn, (long long)M, (long long)rows, (long long)K);
     auto a = make_args(wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, acc);
     return hip_status(wq::launch_gemm(a, static_cast<hipStream_t>(stream)), fn);
 }
@@ -259,7 +265,7 @@ int wq_lm_head_argmax(void* stream, const uint32_t* wq, const uint32_t* ws, int6
     am.ids = ids;
     am.tok_out = tok_out;
     am.keys = static_cast<unsigned long long*>(workspace);
-    am.ticket = reinterpret_cast<unsigned int*>(static_cast<unsigned char*>(workspace) + 64);
+    am.ticket = reinterpret_cast<unsigned int*>(static_cast<unsigned char*>(workspace) + wq::kArgmaxKeyBytes);
     return hip_status(wq::launch_lm_head_argmax(a, am, static_cast<hipStream_t>(stream)), fn);
 }
 

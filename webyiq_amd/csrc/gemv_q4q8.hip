@@ -225,28 +225,53 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         keys[o] = key;
     }
     __syncthreads();
+    // Cross-workgroup combine without fences (a device-scope release would
+    // write back the XCD's L2): keys and tickets live in kArgmaxSlots cache
+    // lines; a workgroup's atomicMax returns before its ticket is taken, and
+    // both are device-coherent atomics, so a ticket implies the max landed.
+    // The last workgroup of each slot takes a top ticket; the last of those
+    // reduces the slots, writes the token and clears the workspace.
+    const int kslot = (int)(blockIdx.x % kArgmaxSlots);
     if (tid < MT && tid < a.M) {
         unsigned long long best = 0;
         for (int rl = 0; rl < RB; ++rl) best = keys[tid * RB + rl] > best ? keys[tid * RB + rl] : best;
-        if (best) atomicMax(p.am.keys + tid, best);
-        __threadfence();
+        const unsigned long long old = atomicMax(p.am.keys + kslot * kArgmaxSlotWords + tid, best);
+        asm volatile("" ::"v"(old));  // the returned value: this atomic has been performed
     }
     __syncthreads();
+    const int used = p.nblocks < kArgmaxSlots ? p.nblocks : kArgmaxSlots;
     if (tid == 0) {
-        unsigned int done = atomicAdd(p.am.ticket, 1u);
-        last_block = done == (unsigned)p.nblocks - 1;
+        const unsigned in_slot = (unsigned)((p.nblocks - kslot + kArgmaxSlots - 1) / kArgmaxSlots);
+        unsigned int done = atomicAdd(p.am.ticket + kslot * kArgmaxSlotWords * 2, 1u);
+        bool last = false;
+        if (done == in_slot - 1) {
+            unsigned int top = atomicAdd(p.am.ticket + kArgmaxSlots * kArgmaxSlotWords * 2, 1u);
+            last = top == (unsigned)used - 1;
+        }
+        last_block = last;
     }
     __syncthreads();
     if (last_block) {
-        __threadfence();
+        // every slot key read at once (independent device-coherent loads),
+        // then reduced in LDS
+        __shared__ unsigned long long slot_keys[kArgmaxSlots * MT];
+        for (int o = tid; o < used * MT; o += nthreads)
+            slot_keys[o] = __hip_atomic_load(p.am.keys + (o / MT) * kArgmaxSlotWords + (o % MT), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
         if (tid < a.M) {
-            unsigned long long k =
-                __hip_atomic_load(p.am.keys + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            unsigned long long k = 0;
+            for (int sl = 0; sl < used; ++sl) k = slot_keys[sl * MT + tid] > k ? slot_keys[sl * MT + tid] : k;
             uint32_t idx = k ? 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull) : 0u;
             p.am.tok_out[tid] = p.am.ids ? p.am.ids[idx] : idx;
-            __hip_atomic_store(p.am.keys + tid, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        if (tid == 0) __hip_atomic_store(p.am.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        for (int o = tid; o < used * MT; o += nthreads)
+            __hip_atomic_store(p.am.keys + (o / MT) * kArgmaxSlotWords + (o % MT), 0ull, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        for (int o = tid; o <= used; o += nthreads)
+            __hip_atomic_store(p.am.ticket + (o < used ? o * kArgmaxSlotWords * 2 : kArgmaxSlots * kArgmaxSlotWords * 2),
+                               0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 

@@ -36,8 +36,8 @@ struct LinearArgs {
 struct ArgmaxArgs {
     const uint32_t* ids;  // nullable id map (draft vocabulary)
     uint32_t* tok_out;    // [M]
-    unsigned long long* keys;  // workspace: [8] running (value, index) keys
-    unsigned int* ticket;      // workspace: blocks-finished counter
+    unsigned long long* keys;  // workspace: [kArgmaxSlots][8] running (value, index) keys
+    unsigned int* ticket;      // workspace: [kArgmaxSlots] slot counters + 1 top counter, one line each
 };
 
 hipError_t launch_quant_act(const QuantArgs& a, hipStream_t s);
@@ -52,7 +52,11 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
 constexpr int kGemvPassK = 2048;
 // Largest token count of the decode GEMV (the M <= 8 speculative-verify case).
 constexpr int kGemvMaxTokens = 8;
-// Workspace of the fused lm_head argmax: 8 keys + ticket, padded.
-constexpr size_t kArgmaxWorkspaceBytes = 128;
+// Workspace of the fused lm_head argmax: kArgmaxSlots cache lines of 8 keys,
+// then kArgmaxSlots + 1 lines holding one counter each.
+constexpr int kArgmaxSlots = 64;
+constexpr int kArgmaxSlotWords = 8;  // 64-bit words per 64-byte line
+constexpr size_t kArgmaxKeyBytes = (size_t)kArgmaxSlots * kArgmaxSlotWords * 8;
+constexpr size_t kArgmaxWorkspaceBytes = kArgmaxKeyBytes + (size_t)(kArgmaxSlots + 1) * 64;
 
 }  // namespace wq
