@@ -173,8 +173,28 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         const float* dr = dx_lds + t * NDX;
         float acc = 0.0f;
         if (PT) {
+            int ee = 0;
+            if ((NE & 3) == 0) {
+                // 16-byte LDS reads, 4 groups per block, all of a block's
+                // operands read before its fma chain (same fma order)
+#pragma unroll 4
+                for (; ee < NE; ee += 4) {
+                    const int4 a4 = *reinterpret_cast<const int4*>(ar + ee);
+                    const float4 x4 = *reinterpret_cast<const float4*>(xsr + ee);
+                    const float4 w01 = *reinterpret_cast<const float4*>(sr + ee);
+                    const float4 w23 = *reinterpret_cast<const float4*>(sr + ee + 2);
+                    acc = fmaf(w01.x, (float)a4.x, acc);
+                    acc = fmaf(w01.y, x4.x, acc);
+                    acc = fmaf(w01.z, (float)a4.y, acc);
+                    acc = fmaf(w01.w, x4.y, acc);
+                    acc = fmaf(w23.x, (float)a4.z, acc);
+                    acc = fmaf(w23.y, x4.z, acc);
+                    acc = fmaf(w23.z, (float)a4.w, acc);
+                    acc = fmaf(w23.w, x4.w, acc);
+                }
+            }
 #pragma unroll 8
-            for (int ee = 0; ee < NE; ++ee) {
+            for (; ee < NE; ++ee) {
                 float2 w = sr[ee];
                 acc = fmaf(w.x, (float)ar[ee], acc);
                 acc = fmaf(w.y, xsr[ee], acc);
