@@ -150,6 +150,26 @@ size_t wq_lm_head_workspace_bytes(void);
 int wq_workspace_clear(void* stream, void* workspace, size_t bytes);
 
 /*
+ * int4 embedding lookup: x[m, :] = dequantised row tok[m] of the packed
+ * matrix (eq, es), x = q * s + m per code (a product, then a sum, as
+ * f32(q) * s.x + s.y in embed.wgsl:13-27).  Replaces the embed op of the
+ * decode and prefill graphs (graph.rs:439-443, 502).  Token ids outside
+ * [0, V) give a zero row.  x f32 [M, K]; K % 128 == 0, G in {32, 128};
+ * eq and x 16-byte aligned.
+ */
+int wq_embed(void* stream, const uint32_t* eq, const uint32_t* es, int64_t V, int64_t K,
+             int32_t G, const uint32_t* tok, int64_t M, float* x);
+
+/*
+ * Row gather of a packed int4 matrix: row r of (dq, ds) = row ids[r] of
+ * (sq, ss).  Replaces the one-time gather of the reduced draft lm_head
+ * (gather_rows.wgsl:13-24, graph.rs:511-516; ids from convert.py:327-330).
+ * Ids outside [0, V) give zero rows.  sq and dq 16-byte aligned.
+ */
+int wq_gather_rows(void* stream, const uint32_t* sq, const uint32_t* ss, int64_t V, int64_t K,
+                   int32_t G, const uint32_t* ids, int64_t R, uint32_t* dq, uint32_t* ds);
+
+/*
  * Test hooks: wq_gemv / wq_gemm that also store the exact int32 group sums
  * A[t, row, e] = sum over group e of q[row, k] * xq[t, k] that the kernel
  * folded into y, into acc i32 [M, rows, K/Ge] (rows = N, or 2N in

@@ -23,7 +23,8 @@ def build():
 def lib():
     global _lib
     if _lib is None:
-        if not os.path.exists(_LIB_PATH):
+        src = os.path.join(_HERE, "q4q8_oracle.c")
+        if not os.path.exists(_LIB_PATH) or os.path.getmtime(_LIB_PATH) < os.path.getmtime(src):
             build()
         L = ctypes.CDLL(_LIB_PATH)
         P = ctypes.c_void_p
@@ -42,6 +43,8 @@ def lib():
         L.or_linear.argtypes = [P, P, i64, i64, i32, P, P, P, i64, i32, i32, P]
         L.or_linear.restype = ctypes.c_int
         L.or_argmax.argtypes = [P, i64, i64, P, P]
+        L.or_embed.argtypes = [P, P, i64, i64, i32, P, i64, P]
+        L.or_gather_rows.argtypes = [P, P, i64, i64, i32, P, i64, P, P]
         _lib = L
     return _lib
 
@@ -160,3 +163,22 @@ def argmax(logits, ids=None):
     idsa = None if ids is None else _c(ids, np.uint32)
     lib().or_argmax(_p(logits), M, N, _p(idsa), _p(out))
     return out
+
+
+def embed(wq, ws, K, G, tok):
+    wq = _c(wq, np.uint32)
+    ws = _c(ws, np.uint32)
+    tok = _c(tok, np.uint32).reshape(-1)
+    x = np.empty((tok.size, K), np.float32)
+    lib().or_embed(_p(wq), _p(ws), wq.shape[0], K, G, _p(tok), tok.size, _p(x))
+    return x
+
+
+def gather_rows(wq, ws, K, G, ids):
+    wq = _c(wq, np.uint32)
+    ws = _c(ws, np.uint32)
+    ids = _c(ids, np.uint32).reshape(-1)
+    dq = np.empty((ids.size, K // 8), np.uint32)
+    ds = np.empty((ids.size, K // G), np.uint32)
+    lib().or_gather_rows(_p(wq), _p(ws), wq.shape[0], K, G, _p(ids), ids.size, _p(dq), _p(ds))
+    return dq, ds

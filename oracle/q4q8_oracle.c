@@ -307,3 +307,43 @@ void or_argmax(const float* logits, int64_t M, int64_t N, const uint32_t* ids,
         tok_out[t] = ids ? ids[idx] : idx;
     }
 }
+
+/* embed.wgsl:13-27.  Word i of a row holds codes 8i..8i+7 (byte b = code
+ * 8i+b | code 8i+4+b << 4); each code is dequantised as f32(q) * s + m with
+ * the (s, m) of its group, the product rounded before the sum. */
+void or_embed(const uint32_t* eq, const uint32_t* es, int64_t V, int64_t K, int G,
+              const uint32_t* tok, int64_t M, float* x) {
+    for (int64_t m = 0; m < M; ++m) {
+        float* xr = x + m * K;
+        const uint32_t t = tok[m];
+        if ((int64_t)t >= V) {
+            for (int64_t k = 0; k < K; ++k) xr[k] = 0.0f;
+            continue;
+        }
+        const uint32_t* qr = eq + (int64_t)t * (K / 8);
+        const uint32_t* sr = es + (int64_t)t * (K / G);
+        for (int64_t i = 0; i < K / 8; ++i) {
+            const uint32_t w = qr[i];
+            for (int b = 0; b < 4; ++b) {
+                const int64_t k0 = 8 * i + b, k1 = 8 * i + 4 + b;
+                const uint32_t s0 = sr[k0 / G], s1 = sr[k1 / G];
+                const float p0 = (float)((w >> (8 * b)) & 15u) * or_f16_to_f32((uint16_t)(s0 & 0xFFFFu));
+                const float p1 = (float)((w >> (8 * b + 4)) & 15u) * or_f16_to_f32((uint16_t)(s1 & 0xFFFFu));
+                xr[k0] = p0 + or_f16_to_f32((uint16_t)(s0 >> 16));
+                xr[k1] = p1 + or_f16_to_f32((uint16_t)(s1 >> 16));
+            }
+        }
+    }
+}
+
+/* gather_rows.wgsl:13-24. */
+void or_gather_rows(const uint32_t* sq, const uint32_t* ss, int64_t V, int64_t K, int G,
+                    const uint32_t* ids, int64_t R, uint32_t* dq, uint32_t* ds) {
+    const int64_t W = K / 8, WS = K / G;
+    for (int64_t r = 0; r < R; ++r) {
+        const uint32_t src = ids[r];
+        const int ok = (int64_t)src < V;
+        for (int64_t i = 0; i < W; ++i) dq[r * W + i] = ok ? sq[(int64_t)src * W + i] : 0u;
+        for (int64_t i = 0; i < WS; ++i) ds[r * WS + i] = ok ? ss[(int64_t)src * WS + i] : 0u;
+    }
+}

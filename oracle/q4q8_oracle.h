@@ -61,6 +61,16 @@ int or_linear(const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K, int 
 void or_argmax(const float* logits, int64_t M, int64_t N, const uint32_t* ids,
                uint32_t* tok_out);
 
+/* int4 embedding lookup (embed.wgsl:13-27): x[m, k] = f32(q) * s + m of row
+ * tok[m] (a product, then a sum); ids outside [0, V) give a zero row. */
+void or_embed(const uint32_t* eq, const uint32_t* es, int64_t V, int64_t K, int G,
+              const uint32_t* tok, int64_t M, float* x);
+
+/* Packed row gather (gather_rows.wgsl:13-24): dst row r = src row ids[r];
+ * ids outside [0, V) give zero rows. */
+void or_gather_rows(const uint32_t* sq, const uint32_t* ss, int64_t V, int64_t K, int G,
+                    const uint32_t* ids, int64_t R, uint32_t* dq, uint32_t* ds);
+
 #ifdef __cplusplus
 }
 #endif

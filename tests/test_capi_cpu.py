@@ -21,7 +21,7 @@ def declared_symbols():
 
 def test_exports_every_declared_symbol():
     names = declared_symbols()
-    assert len(names) == 12
+    assert len(names) == 14
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(_lib.PROTOTYPES)
@@ -96,3 +96,17 @@ def test_python_wrapper_raises_wq_error():
     with pytest.raises(_lib.WqError) as e:
         _lib.call("wq_gemv", None, None, A4, 64, 2048, 128, A16, A4, A4, 1, 2048, 0, A4)
     assert e.value.code == _lib.WQ_EINVAL and "wq is NULL" in e.value.message
+
+
+def test_embed_and_gather_errors():
+    e = L.wq_embed
+    assert e(None, None, A4, 100, 2048, 32, A4, 1, A16) == _lib.WQ_EINVAL and "eq is NULL" in err()
+    assert e(None, A16, A4, 100, 2000, 32, A4, 1, A16) == _lib.WQ_ESHAPE
+    assert e(None, A16, A4, 100, 2048, 64, A4, 1, A16) == _lib.WQ_ESHAPE
+    assert e(None, A16, A4, 0, 2048, 32, A4, 1, A16) == _lib.WQ_ESHAPE
+    assert e(None, A16, A4, 100, 2048, 32, A4, 0, A16) == _lib.WQ_ESHAPE
+    assert e(None, A16, A4, 100, 2048, 32, A4, 1, A4) == _lib.WQ_EALIGN
+    g = L.wq_gather_rows
+    assert g(None, A16, A4, 100, 2048, 128, None, 4, A16, A4) == _lib.WQ_EINVAL
+    assert g(None, A16, A4, 100, 2048, 128, A4, 0, A16, A4) == _lib.WQ_ESHAPE
+    assert g(None, A16, A4, 100, 2048, 128, A4, 4, A4, A4) == _lib.WQ_EALIGN

@@ -305,3 +305,45 @@ def test_decode_mlp_block():
     gu = ref.FakeQuantLinear(wgu, sgu, hd, 128, mode=2)(x)
     out = ref.FakeQuantLinear(wd, sd, ffn, 128, mode=1)(gu, resid).numpy()
     assert rel_err(host(y), out) < 1e-3
+
+
+# ------------------------------------------------ embedding, row gather ----
+
+@pytest.mark.parametrize("G,M", [(32, 1), (128, 2), (32, 7), (128, 33)])
+def test_embed_bit_exact(G, M):
+    """int4 embedding lookup (embed.wgsl) against the oracle, bit for bit;
+    ids past the vocabulary give zero rows."""
+    note(f"embed G={G} M={M}")
+    V, K = 4096, 2048
+    rng = np.random.default_rng(G + M)
+    wq, ws = ref.make_weight(rng, V, K, G)
+    tok = rng.integers(0, V, M).astype(np.uint32)
+    tok[-1] = V + 5 if M > 1 else tok[-1]
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
+    x = host(ops.embed(w, dev(tok.view(np.int32))))
+    want = orc.embed(wq, ws, K, G, tok)
+    assert np.array_equal(x.view(np.uint32), want.view(np.uint32))
+
+
+def test_gather_rows_and_draft_head():
+    """The reduced draft lm_head (graph.rs:511-522): gather the rows of the
+    ascending draft ids, then the fused lm_head + argmax over them maps the
+    winner back through ids -- the same token as the argmax of the full
+    head's logits restricted to those rows."""
+    note("gather rows + draft head")
+    V, K, G, R = 20000, 2048, 128, 3000
+    rng = np.random.default_rng(11)
+    wq, ws = ref.make_weight(rng, V, K, G)
+    ids = np.sort(rng.choice(V, R, replace=False)).astype(np.uint32)
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
+    d = ops.gather_rows(w, dev(ids.view(np.int32)))
+    assert np.array_equal(host(d.q).view(np.uint32), wq[ids])
+    assert np.array_equal(host(d.s).view(np.uint32), ws[ids])
+    bad = ops.gather_rows(w, dev(np.array([3, V], np.uint32).view(np.int32)))
+    assert np.array_equal(host(bad.q).view(np.uint32)[0], wq[3]) and not np.any(host(bad.q)[1])
+    x = ref.make_activations(rng, 2, K)
+    xq, dx, xs = orc.quant_act(x, None, G)
+    a = dev_acts(xq, dx, xs, K, G)
+    tok = host(ops.lm_head_argmax(d, a, ids=dev(ids.view(np.int32))))
+    logits = orc.linear(wq[ids], ws[ids], K, G, xq, dx, xs)
+    assert np.array_equal(tok.view(np.uint32), orc.argmax(logits, ids))

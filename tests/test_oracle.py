@@ -239,3 +239,41 @@ def test_argmax_first_occurrence_and_ties(rng):
     assert out[5] == 0
     ids = np.arange(5000, dtype=np.uint32) * 3 + 1
     assert np.array_equal(orc.argmax(v, ids), ids[out])
+
+
+# ------------------------------------------------- embedding, row gather ----
+
+def _numpy_dequant_rows(wq, ws, K, G, rows):
+    """embed.wgsl:19-27 restated with numpy bit operations (not the oracle's
+    unpacker): byte b of word i holds code 8i+b (low nibble) and 8i+4+b."""
+    w = wq[rows].astype(np.uint32)                       # [R, K/8]
+    lo = np.stack([(w >> (8 * b)) & 15 for b in range(4)], -1)
+    hi = np.stack([(w >> (8 * b + 4)) & 15 for b in range(4)], -1)
+    q = np.concatenate([lo, hi], -1).reshape(len(rows), K).astype(np.float32)
+    s = (ws[rows] & 0xFFFF).astype(np.uint16).view(np.float16).astype(np.float32)
+    m = (ws[rows] >> 16).astype(np.uint16).view(np.float16).astype(np.float32)
+    s = np.repeat(s, G, axis=1)
+    m = np.repeat(m, G, axis=1)
+    return (q * s) + m                                   # product rounded, then the sum
+
+
+@pytest.mark.parametrize("G", [32, 128])
+def test_embed_matches_numpy_dequant(rng, G):
+    V, K = 300, 512
+    wq, ws = ref.make_weight(rng, V, K, G)
+    tok = np.array([0, 299, 17, 17, 150], np.uint32)
+    x = orc.embed(wq, ws, K, G, tok)
+    assert np.array_equal(x.view(np.uint32), _numpy_dequant_rows(wq, ws, K, G, tok).view(np.uint32))
+    # an id past the vocabulary gives a zero row
+    x2 = orc.embed(wq, ws, K, G, np.array([V, 2**32 - 1], np.uint32))
+    assert not np.any(x2)
+
+
+def test_gather_rows_is_row_indexing(rng):
+    V, K, G = 200, 1024, 128
+    wq, ws = ref.make_weight(rng, V, K, G)
+    ids = np.sort(rng.choice(V, 64, replace=False)).astype(np.uint32)   # ascending (convert.py:328)
+    dq, ds = orc.gather_rows(wq, ws, K, G, ids)
+    assert np.array_equal(dq, wq[ids]) and np.array_equal(ds, ws[ids])
+    dq, ds = orc.gather_rows(wq, ws, K, G, np.array([5, V + 3], np.uint32))
+    assert np.array_equal(dq[0], wq[5]) and not np.any(dq[1]) and not np.any(ds[1])

@@ -42,6 +42,8 @@ PROTOTYPES = {
                           ctypes.c_int),
     "wq_lm_head_workspace_bytes": ([], _SZ),
     "wq_workspace_clear": ([_P, _P, _SZ], ctypes.c_int),
+    "wq_embed": ([_P, _P, _P, _I64, _I64, _I32, _P, _I64, _P], ctypes.c_int),
+    "wq_gather_rows": ([_P, _P, _P, _I64, _I64, _I32, _P, _I64, _P, _P], ctypes.c_int),
 }
 
 

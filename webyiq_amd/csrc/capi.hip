@@ -235,6 +235,50 @@ int wq_argmax(void* stream, const float* logits, int64_t M, int64_t V, const uin
     return hip_status(wq::launch_argmax(logits, M, V, ids, tok_out, static_cast<hipStream_t>(stream)), fn);
 }
 
+int wq_embed(void* stream, const uint32_t* eq, const uint32_t* es, int64_t V, int64_t K, int32_t G,
+             const uint32_t* tok, int64_t M, float* x) {
+    const char* fn = "wq_embed";
+    REQUIRE_PTR(eq);
+    REQUIRE_PTR(es);
+    REQUIRE_PTR(tok);
+    REQUIRE_PTR(x);
+    if (V < 1 || V > (int64_t)0xFFFFFFFFll)
+        return fail(WQ_ESHAPE, "%s: V = %lld out of range", fn, (long long)V);
+    if (M < 1 || M > (int64_t(1) << 30))
+        return fail(WQ_ESHAPE, "%s: M = %lld out of range", fn, (long long)M);
+    int rc = check_groups(fn, K, G, (int32_t)K);
+    if (rc) return rc;
+    REQUIRE_ALIGN(eq, 16);
+    REQUIRE_ALIGN(es, 4);
+    REQUIRE_ALIGN(tok, 4);
+    REQUIRE_ALIGN(x, 16);
+    wq::EmbedArgs a{eq, es, V, K, G, tok, M, x};
+    return hip_status(wq::launch_embed(a, static_cast<hipStream_t>(stream)), fn);
+}
+
+int wq_gather_rows(void* stream, const uint32_t* sq, const uint32_t* ss, int64_t V, int64_t K,
+                   int32_t G, const uint32_t* ids, int64_t R, uint32_t* dq, uint32_t* ds) {
+    const char* fn = "wq_gather_rows";
+    REQUIRE_PTR(sq);
+    REQUIRE_PTR(ss);
+    REQUIRE_PTR(ids);
+    REQUIRE_PTR(dq);
+    REQUIRE_PTR(ds);
+    if (V < 1 || V > (int64_t)0xFFFFFFFFll)
+        return fail(WQ_ESHAPE, "%s: V = %lld out of range", fn, (long long)V);
+    if (R < 1 || R > (int64_t(1) << 30))
+        return fail(WQ_ESHAPE, "%s: R = %lld out of range", fn, (long long)R);
+    int rc = check_groups(fn, K, G, (int32_t)K);
+    if (rc) return rc;
+    REQUIRE_ALIGN(sq, 16);
+    REQUIRE_ALIGN(dq, 16);
+    REQUIRE_ALIGN(ss, 4);
+    REQUIRE_ALIGN(ds, 4);
+    REQUIRE_ALIGN(ids, 4);
+    wq::GatherArgs a{sq, ss, V, K, G, ids, R, dq, ds};
+    return hip_status(wq::launch_gather_rows(a, static_cast<hipStream_t>(stream)), fn);
+}
+
 size_t wq_lm_head_workspace_bytes(void) { return wq::kArgmaxWorkspaceBytes; }
 
 int wq_workspace_clear(void* stream, void* workspace, size_t bytes) {

@@ -40,7 +40,30 @@ struct ArgmaxArgs {
     unsigned int* ticket;      // workspace: [kArgmaxSlots] slot counters + 1 top counter, one line each
 };
 
+struct EmbedArgs {
+    const uint32_t* q;    // [V, K/8] packed int4 rows
+    const uint32_t* s;    // [V, K/G] (scale, min) words
+    int64_t V, K;
+    int G;
+    const uint32_t* ids;  // [M] token ids
+    int64_t M;
+    float* x;             // [M, K]
+};
+
+struct GatherArgs {
+    const uint32_t* q;    // source [V, K/8]
+    const uint32_t* s;    // source [V, K/G]
+    int64_t V, K;
+    int G;
+    const uint32_t* ids;  // [R] source rows
+    int64_t R;
+    uint32_t* dq;         // [R, K/8]
+    uint32_t* ds;         // [R, K/G]
+};
+
 hipError_t launch_quant_act(const QuantArgs& a, hipStream_t s);
+hipError_t launch_embed(const EmbedArgs& a, hipStream_t s);
+hipError_t launch_gather_rows(const GatherArgs& a, hipStream_t s);
 hipError_t launch_gemv(const LinearArgs& a, hipStream_t s);
 hipError_t launch_lm_head_argmax(const LinearArgs& a, const ArgmaxArgs& am, hipStream_t s);
 hipError_t launch_gemm(const LinearArgs& a, hipStream_t s);

@@ -181,3 +181,22 @@ def lm_head_argmax(w: Q4Tensor, a: Acts, ids=None, logits=None, workspace=None, 
               _ptr(a.xq), _ptr(a.dx), _ptr(a.xs), a.M, a.GA, _ptr(ids), _ptr(logits),
               _ptr(out), _ptr(workspace), workspace.numel())
     return out
+
+
+def embed(w: Q4Tensor, tok, out=None, stream=None):
+    """int4 embedding lookup (embed.wgsl): x[m] = dequantised row tok[m]."""
+    M = tok.numel()
+    x = torch.empty((M, w.K), dtype=torch.float32, device=tok.device) if out is None else out
+    _lib.call("wq_embed", _stream(stream), _ptr(w.q), _ptr(w.s), w.rows, w.K, w.G, _ptr(tok), M, _ptr(x))
+    return x
+
+
+def gather_rows(w: Q4Tensor, ids, stream=None) -> Q4Tensor:
+    """Packed rows ids of w as a new Q4Tensor (gather_rows.wgsl: the reduced
+    draft lm_head)."""
+    R = ids.numel()
+    dq = torch.empty((R, w.K // 8), dtype=torch.int32, device=ids.device)
+    ds = torch.empty((R, w.K // w.G), dtype=torch.int32, device=ids.device)
+    _lib.call("wq_gather_rows", _stream(stream), _ptr(w.q), _ptr(w.s), w.rows, w.K, w.G, _ptr(ids), R,
+              _ptr(dq), _ptr(ds))
+    return Q4Tensor(dq, ds, w.K, w.G)
