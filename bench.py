@@ -314,6 +314,18 @@ def bench_configs(torch, lib, ops):
     a2 = ops.empty_acts(1, F, None, G)
     h = torch.empty((1, F), dtype=torch.float32, device="cuda")
     yres = torch.zeros((1, K1), dtype=torch.float32, device="cuda")
+    fused = []
+    for (qg, sg), (qd, sd) in zip(gu, dn):
+        fused.append(Launcher(lib, "wq_quant_gemv", [P(x.data_ptr()), P(nw.data_ptr()), ctypes.c_float(1e-6),
+                                                     P(qg.data_ptr()), P(sg.data_ptr()), F, K1, G, 1, 2,
+                                                     P(a1.xq.data_ptr()), P(a1.dx.data_ptr()), P(a1.xs.data_ptr()),
+                                                     P(h.data_ptr())]))
+        fused.append(Launcher(lib, "wq_quant_gemv", [P(h.data_ptr()), None, ctypes.c_float(0.0),
+                                                     P(qd.data_ptr()), P(sd.data_ptr()), K1, F, G, 1, 1,
+                                                     P(a2.xq.data_ptr()), P(a2.dx.data_ptr()), P(a2.xs.data_ptr()),
+                                                     P(yres.data_ptr())]))
+    graph_time(torch, fused, 2)
+    t2 = graph_time(torch, fused, max(2, 128 // R)) * 2  # per block (2 launches)
     steps = []
     for (qg, sg), (qd, sd) in zip(gu, dn):
         steps.append(Launcher(lib, "wq_quant_act", [P(x.data_ptr()), P(nw.data_ptr()), ctypes.c_float(1e-6), 1, K1,
@@ -327,8 +339,9 @@ def bench_configs(torch, lib, ops):
     graph_time(torch, steps, 2)
     t4 = graph_time(torch, steps, max(2, 128 // R)) * 4  # per block (4 launches)
     nb_block = nb_gu + nb_q + nb_dn
-    res["cfg2_decode_mlp_block"] = {"us": round(t4 * 1e6, 3), "bytes": nb_block,
-                                    "GBps": round(nb_block / t4 / 1e9, 1), "launches": 4}
+    res["cfg2_decode_mlp_block"] = {"us": round(t2 * 1e6, 3), "bytes": nb_block,
+                                    "GBps": round(nb_block / t2 / 1e9, 1), "launches": 2,
+                                    "unfused_us": round(t4 * 1e6, 3), "unfused_launches": 4}
     del gu, dn
 
     # cfg 5: lm_head + fused argmax, M = 1 and 8, V = 151936 and 32768
@@ -352,6 +365,40 @@ def bench_configs(torch, lib, ops):
                                   "frac_hbm": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)}
         del ws
     res["cfg5_lm_head_argmax"] = head
+
+    # decode step capture: 20 layers' linear sequences in one HIP graph
+    # (webyiq_amd/layer.py: qkv, o, gate_up, down with their quantisers), the
+    # layers sharing one residual stream
+    from webyiq_amd.layer import DecodeLayer
+    H, Q, KV, F, L = 2048, 2048, 512, 6144, 20
+    step = {}
+    for M, fuse in ((1, True), (2, True), (1, False)):
+        x = torch.zeros((M, H), dtype=torch.float32, device="cuda")
+        layers = []
+        for _ in range(L):
+            w = ops.Weights()
+            for name, (r, c) in {"qkv": (Q + 2 * KV, H), "o": (H, Q), "gate_up": (2 * F, H),
+                                 "down": (H, F)}.items():
+                (q, sc), = rand_weights(torch, r, c, G, 1)
+                w[name] = ops.Q4Tensor(q, sc, c, G)
+            w["attn_norm"] = torch.ones(H, dtype=torch.float32, device="cuda")
+            w["mlp_norm"] = torch.ones(H, dtype=torch.float32, device="cuda")
+            layers.append(DecodeLayer(w, M, hidden=H, q_dim=Q, kv_dim=KV, ffn=F, G=G, fused=fuse, x=x))
+        x0 = torch.randn((M, H), dtype=torch.float32, device="cuda")
+
+        class Step:  # the graph_time launch protocol: one callable per captured unit
+            def __call__(self, stream):
+                x.copy_(x0)
+                for lay in layers:
+                    lay.run()
+        graph_time(torch, [Step()], 2)
+        t = graph_time(torch, [Step()], 10)
+        nbw = sum(lay.weight_bytes() for lay in layers)
+        step[f"M{M}" + ("" if fuse else "_unfused")] = {
+            "us_per_layer": round(t / L * 1e6, 3), "layers": L, "launches_per_layer": 5 if fuse else 9,
+            "weight_GBps": round(nbw / t / 1e9, 1)}
+        del layers
+    res["decode_step_graph"] = step
     torch.cuda.empty_cache()
     return res
 

@@ -77,7 +77,7 @@ int wq_abi_version(void);
  *   xs[e] = sum of xq over accumulation group e of Ge = min(G, GA) elements
  * x f32 [M, K], norm_w f32 [K] or NULL.  GA in {32, K}; G in {32, 128} is
  * the weight group of the linear layer that will consume xq.
- * Requires K % 128 == 0; x, norm_w 16-byte aligned; xq 4-byte aligned.
+ * Requires K % 128 == 0; x, norm_w and xq 16-byte aligned.
  */
 int wq_quant_act(void* stream, const float* x, const float* norm_w, float eps,
                  int64_t M, int64_t K, int32_t GA, int32_t G,
@@ -94,6 +94,22 @@ int wq_quant_act(void* stream, const float* x, const float* norm_w, float eps,
 int wq_gemv(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K,
             int32_t G, const int8_t* xq, const float* dx, const int32_t* xs,
             int64_t M, int32_t GA, int32_t mode, float* y);
+
+/*
+ * Quantiser + decode GEMV, 1 <= M <= 8, per-token activation scales
+ * (GA = K).  Replaces the quant -> matmul pairs of the decode layer
+ * (graph.rs:266+269, 285+293, 304+305, 313+314, 323+324, 325+326) and of the
+ * head (graph.rs:482-483).  y and the quantised activations xq i8 [M, K],
+ * dx f32 [M], xs i32 [M, K/G] (required outputs, read by the products that
+ * share the input) are bit-identical to wq_quant_act(GA = K) followed by
+ * wq_gemv.  M <= 2 is one launch: every workgroup quantises the tokens while
+ * its weight loads are in flight, and workgroup 0 writes xq/dx/xs; larger M
+ * is those two launches.  y must not overlap x.  Requirements of wq_gemv and
+ * wq_quant_act (x, norm_w 16-byte aligned).
+ */
+int wq_quant_gemv(void* stream, const float* x, const float* norm_w, float eps,
+                  const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K, int32_t G,
+                  int64_t M, int32_t mode, int8_t* xq, float* dx, int32_t* xs, float* y);
 
 /*
  * Prefill GEMM, any M >= 1 (tiles of 128 tokens).  Replaces Builder::gemm

@@ -149,21 +149,30 @@ void or_q4_quantize(const float* w, int64_t N, int64_t K, int G,
 
 /* --------------------------------------------------- activation quant ---- */
 
-/* RMSNorm prologue in the kernel's reduction order: 256 partial sums, lane i
- * owning float4 chunks i, i+256, ... (each element added by fmaf in index
- * order), then a halving tree p[i] += p[i+s] for s = 128..1.
+/* RMSNorm prologue in the kernels' reduction order.  The row is cut into
+ * 32-element slices (one GPU lane each); a slice's partial is an fmaf chain
+ * over its elements in index order.  The 64 slices of each 2048-element pass
+ * (one wavefront) are combined by a pairwise tree with offsets 1, 2, ..., 32
+ * (p[i] += p[i + o] for i with bit o clear: the wavefront's xor butterfly),
+ * slices past K counting as 0; the pass sums are then added in pass order.
  * quant.wgsl:24-39: r = 1/sqrt(mean(x^2) + eps); v = (x * r) * nw. */
 static float rms_scale(const float* x, int64_t K, float eps) {
-    float p[256];
-    for (int i = 0; i < 256; ++i) {
-        float acc = 0.0f;
-        for (int64_t c = i; c < K / 4; c += 256)
-            for (int j = 0; j < 4; ++j) acc = fmaf(x[4 * c + j], x[4 * c + j], acc);
-        p[i] = acc;
+    float total = 0.0f;
+    for (int64_t j = 0; 2048 * j < K; ++j) {
+        float p[64];
+        for (int l = 0; l < 64; ++l) {
+            const int64_t b = 2048 * j + 32 * l;
+            float acc = 0.0f;
+            if (b < K)
+                for (int i = 0; i < 32; ++i) acc = fmaf(x[b + i], x[b + i], acc);
+            p[l] = acc;
+        }
+        for (int o = 1; o < 64; o <<= 1)
+            for (int i = 0; i < 64; ++i)
+                if (!(i & o)) p[i] = p[i] + p[i + o];
+        total = total + p[0];
     }
-    for (int s = 128; s > 0; s >>= 1)
-        for (int i = 0; i < s; ++i) p[i] = p[i] + p[i + s];
-    return 1.0f / sqrtf(p[0] / (float)K + eps);
+    return 1.0f / sqrtf(total / (float)K + eps);
 }
 
 /* quant.wgsl:41-61 and tools/reference.py:43-48 (fq_input):

@@ -21,7 +21,7 @@ def declared_symbols():
 
 def test_exports_every_declared_symbol():
     names = declared_symbols()
-    assert len(names) == 14
+    assert len(names) == 15
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(_lib.PROTOTYPES)
@@ -78,6 +78,27 @@ def test_quant_errors():
     assert q(None, A16, None, 1e-6, 1, 2048, 64, 128, A16, A4, A4) == _lib.WQ_ESHAPE
     assert q(None, A4, None, 1e-6, 1, 2048, 2048, 128, A16, A4, A4) == _lib.WQ_EALIGN
     assert q(None, A16, A16, -1.0, 1, 2048, 2048, 128, A16, A4, A4) == _lib.WQ_EINVAL
+    assert q(None, A16, None, 1e-6, 1, 2048, 2048, 128, A4, A4, A4) == _lib.WQ_EALIGN and "xq" in err()
+
+
+def test_quant_gemv_errors():
+    f = L.wq_quant_gemv
+
+    def call(x=A16, nw=None, eps=1e-6, wq=A16, N=64, K=2048, G=128, M=1, mode=0, xq=A16, dx=A4, xs=A4, y=A4):
+        return f(None, x, nw, eps, wq, A4, N, K, G, M, mode, xq, dx, xs, y)
+
+    assert call(x=None) == _lib.WQ_EINVAL and "x is NULL" in err()
+    assert call(xq=None) == _lib.WQ_EINVAL  # the activations are required outputs
+    assert call(y=None) == _lib.WQ_EINVAL
+    assert call(M=9) == _lib.WQ_ESHAPE and "M = 9" in err()
+    assert call(M=0) == _lib.WQ_ESHAPE
+    assert call(K=2000) == _lib.WQ_ESHAPE
+    assert call(K=2048 * 9) == _lib.WQ_ESHAPE
+    assert call(G=64) == _lib.WQ_ESHAPE
+    assert call(x=A4) == _lib.WQ_EALIGN and "x not 16" in err()
+    assert call(nw=A4) == _lib.WQ_EALIGN
+    assert call(nw=A16, eps=-1.0) == _lib.WQ_EINVAL and "eps" in err()
+    assert call(mode=3) == _lib.WQ_EINVAL
 
 
 def test_argmax_and_lm_head_errors():

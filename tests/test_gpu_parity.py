@@ -55,6 +55,7 @@ def setup_linear(seed, M, K, rows, G, GA):
     (1, 2048, None, 128, False), (3, 6144, None, 128, False), (8, 2048, None, 32, False),
     (5, 1024, 32, 128, False), (2, 128, None, 128, False), (64, 2048, None, 128, False),
     (4, 2048, None, 128, True), (3, 6144, 32, 32, True),
+    (1, 2176, None, 32, True), (2, 10240, None, 128, True),   # partial pass; rows past 4 passes
 ])
 def test_quant_act_bit_exact(M, K, GA, G, norm):
     note(f"quant M={M} K={K} GA={GA} G={G} norm={norm}")
@@ -307,6 +308,51 @@ def test_decode_mlp_block():
     assert rel_err(host(y), out) < 1e-3
 
 
+# ------------------------------------------- fused quantiser + GEMV -------
+
+QUANT_GEMV_CASES = [
+    # M, K, N, G, mode, norm
+    (1, 2048, 6144, 128, 0, True),   # norm_quant -> qkv / lm_head shape
+    (1, 6144, 2048, 128, 1, False),  # quant -> down (+= residual)
+    (2, 2048, 6144, 128, 2, True),   # norm_quant -> gate_up (SiLU * up)
+    (1, 128, 77, 128, 0, False),     # one group, partial pass
+    (2, 3072, 96, 32, 0, True),      # K not a multiple of 2048, G = 32
+    (1, 16384, 256, 128, 1, True),   # eight passes
+    (5, 2048, 512, 128, 0, True),    # M > 2: quantiser and GEMV launches
+]
+
+
+@pytest.mark.parametrize("M,K,N,G,mode,norm", QUANT_GEMV_CASES)
+def test_quant_gemv_bit_exact(M, K, N, G, mode, norm):
+    """quant -> matmul pairs of the decode layer in one call: y and the
+    quantised activations are bit-identical to wq_quant_act + wq_gemv, and
+    match the oracle (bit-exact; mode 2 within rel 1e-5, device expf)."""
+    note(f"quant_gemv M={M} K={K} N={N} G={G} mode={mode} norm={norm}")
+    rng = np.random.default_rng(M * 100 + K + N)
+    rows = 2 * N if mode == 2 else N
+    wq, ws = ref.make_weight(rng, rows, K, G)
+    x = ref.make_activations(rng, M, K)
+    nw = rng.normal(1.0, 0.2, size=K).astype(np.float32) if norm else None
+    y0 = rng.normal(size=(M, N)).astype(np.float32)
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
+    dnw = None if nw is None else dev(nw)
+    y = dev(y0) if mode == 1 else None
+    y, a = ops.quant_gemv(w, dev(x), norm=dnw, eps=1e-6, mode=mode, y=y)
+    a2 = ops.quant(dev(x), norm=dnw, eps=1e-6, G=G)
+    y2 = ops.gemv(w, a2, mode=mode, y=dev(y0) if mode == 1 else None)
+    assert np.array_equal(host(a.xq), host(a2.xq))
+    assert np.array_equal(host(a.dx).view(np.uint32), host(a2.dx).view(np.uint32))
+    assert np.array_equal(host(a.xs), host(a2.xs))
+    assert np.array_equal(host(y).view(np.uint32), host(y2).view(np.uint32))
+    xq, dx, xs = orc.quant_act(x, None, G, norm_w=nw, eps=1e-6)
+    assert np.array_equal(host(a.xq), xq)
+    want = orc.linear(wq, ws, K, G, xq, dx, xs, mode=mode, y=y0 if mode == 1 else None)
+    if mode == 2:
+        assert rel_err(host(y), want) < 1e-5
+    else:
+        assert np.array_equal(host(y).view(np.uint32), want.view(np.uint32))
+
+
 # ------------------------------------------------ embedding, row gather ----
 
 @pytest.mark.parametrize("G,M", [(32, 1), (128, 2), (32, 7), (128, 33)])
@@ -347,3 +393,55 @@ def test_gather_rows_and_draft_head():
     tok = host(ops.lm_head_argmax(d, a, ids=dev(ids.view(np.int32))))
     logits = orc.linear(wq[ids], ws[ids], K, G, xq, dx, xs)
     assert np.array_equal(tok.view(np.uint32), orc.argmax(logits, ids))
+
+
+# ------------------------------------------------- decode-layer capture -----
+
+def test_decode_layer_graph_replay():
+    """One layer's linear sequence (graph.rs:257-328) recorded into a HIP graph
+    and replayed (lib.rs:222-228): every replay, with eager work between them,
+    reproduces the eager run bit for bit; the fused sequence equals the
+    unfused one (separate quantiser launches) bit for bit; the first
+    projection matches the oracle bit for bit."""
+    from webyiq_amd.layer import DecodeLayer
+    note("decode layer graph replay")
+    M, H, Q, KV, F, G = 2, 1024, 1024, 256, 2048, 128
+    rng = np.random.default_rng(21)
+    shapes = {"qkv": (Q + 2 * KV, H), "o": (H, Q), "gate_up": (2 * F, H), "down": (H, F)}
+    host_w = {n: ref.make_weight(rng, r, c, G) for n, (r, c) in shapes.items()}
+    w = ops.Weights({n: ops.Q4Tensor.from_numpy(q, s, shapes[n][1], G) for n, (q, s) in host_w.items()})
+    w["attn_norm"] = dev(rng.normal(1, 0.1, H).astype(np.float32))
+    w["mlp_norm"] = dev(rng.normal(1, 0.1, H).astype(np.float32))
+    x0 = dev(ref.make_activations(rng, M, H))
+
+    plain = DecodeLayer(w, M, hidden=H, q_dim=Q, kv_dim=KV, ffn=F, G=G, fused=False)
+    plain.x.copy_(x0)
+    plain.run()
+    layer = DecodeLayer(w, M, hidden=H, q_dim=Q, kv_dim=KV, ffn=F, G=G)
+    layer.x.copy_(x0)
+    layer.run()
+    want = host(layer.x).copy()
+    assert np.array_equal(want.view(np.uint32), host(plain.x).view(np.uint32))
+    # first projection against the oracle, bit for bit
+    xq, dx, xs = orc.quant_act(host(x0), None, G, norm_w=host(w["attn_norm"]), eps=1e-6)
+    qkv_want = orc.linear(*host_w["qkv"], H, G, xq, dx, xs)
+    assert np.array_equal(host(layer.qkv).view(np.uint32), qkv_want.view(np.uint32))
+    assert np.all(np.isfinite(want))
+
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        layer.x.copy_(x0)
+        layer.run()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        layer.x.copy_(x0)
+        layer.run()
+    for i in range(3):
+        g.replay()
+        got = host(layer.x)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"replay {i}"
+        ops.quant(dev(rng.normal(size=(3, 256)).astype(np.float32)))   # eager work between replays
+        torch.cuda.synchronize()

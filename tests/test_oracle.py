@@ -137,10 +137,12 @@ def test_quant_act_amax_maps_to_127(rng):
     assert np.all(np.abs(xq[np.arange(4), np.abs(x).argmax(1)]) == 127)
 
 
-def test_quant_act_rmsnorm_prologue(rng):
-    """quant.wgsl:24-39: v = x * nw / sqrt(mean(x^2) + eps); checked in float64."""
-    x = rng.normal(0, 3, size=(3, 2048)).astype(np.float32)
-    nw = rng.normal(1, 0.1, size=2048).astype(np.float32)
+@pytest.mark.parametrize("K", [128, 2048, 2176, 6144])
+def test_quant_act_rmsnorm_prologue(rng, K):
+    """quant.wgsl:24-39: v = x * nw / sqrt(mean(x^2) + eps); checked in float64
+    (partial and several 2048-element passes: every element counted once)."""
+    x = rng.normal(0, 3, size=(3, K)).astype(np.float32)
+    nw = rng.normal(1, 0.1, size=K).astype(np.float32)
     xq, dx, _ = orc.quant_act(x, None, 128, norm_w=nw, eps=1e-6)
     v = x.astype(np.float64) / np.sqrt((x.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6) * nw
     d = np.abs(v).max(1) / 127

@@ -168,7 +168,7 @@ int wq_quant_act(void* stream, const float* x, const float* norm_w, float eps, i
     if (K > (int64_t(1) << 24)) return fail(WQ_ESHAPE, "%s: K = %lld too large", fn, (long long)K);
     REQUIRE_ALIGN(x, 16);
     if (norm_w) REQUIRE_ALIGN(norm_w, 16);
-    REQUIRE_ALIGN(xq, 4);
+    REQUIRE_ALIGN(xq, 16);
     REQUIRE_ALIGN(dx, 4);
     REQUIRE_ALIGN(xs, 4);
     if (norm_w && !(eps >= 0.0f)) return fail(WQ_EINVAL, "%s: eps must be >= 0", fn);
@@ -180,6 +180,30 @@ int wq_gemv(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int
             const int8_t* xq, const float* dx, const int32_t* xs, int64_t M, int32_t GA,
             int32_t mode, float* y) {
     return gemv_impl("wq_gemv", stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, nullptr);
+}
+
+int wq_quant_gemv(void* stream, const float* x, const float* norm_w, float eps, const uint32_t* wq,
+                  const uint32_t* ws, int64_t N, int64_t K, int32_t G, int64_t M, int32_t mode,
+                  int8_t* xq, float* dx, int32_t* xs, float* y) {
+    const char* fn = "wq_quant_gemv";
+    REQUIRE_PTR(x);
+    int rc = check_gemv_shape(fn, M, K);
+    if (rc) return rc;
+    rc = check_linear(fn, wq, ws, N, K, G, xq, dx, xs, M, (int32_t)K, mode, y, true);
+    if (rc) return rc;
+    REQUIRE_ALIGN(x, 16);
+    if (norm_w) REQUIRE_ALIGN(norm_w, 16);
+    if (norm_w && !(eps >= 0.0f)) return fail(WQ_EINVAL, "%s: eps must be >= 0", fn);
+    auto a = make_args(wq, ws, N, K, G, xq, dx, xs, M, (int32_t)K, mode, y, nullptr);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (M <= 2) {  // one launch: every workgroup quantises while its weights stream in
+        wq::QuantInArgs q{x, norm_w, eps, xq, dx, xs};
+        return hip_status(wq::launch_gemv_quant_in(a, q, st), fn);
+    }
+    wq::QuantArgs qa{x, norm_w, eps, M, K, (int32_t)K, G, xq, dx, xs};
+    rc = hip_status(wq::launch_quant_act(qa, st), fn);
+    if (rc) return rc;
+    return hip_status(wq::launch_gemv(a, st), fn);
 }
 
 int wq_gemm(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K, int32_t G,

@@ -91,4 +91,23 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) 
     return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
 }
 
+// Correctly rounded single-precision square root: the hardware estimate is
+// within one ulp, and the candidate with the smallest |x - c^2| (exact in
+// double: c^2 has 48 significant bits) is the rounded root (a square root is
+// never exactly halfway between two floats).
+__device__ float sqrt_rn(float x) {
+    float y = __builtin_amdgcn_sqrtf(x);
+    if (!(x > 0.0f) || isinf(x) || !(y > 0.0f)) return y;
+    float lo = __uint_as_float(__float_as_uint(y) - 1u);
+    float hi = __uint_as_float(__float_as_uint(y) + 1u);
+    double xd = (double)x;
+    double ey = fabs(xd - (double)y * (double)y);
+    double el = fabs(xd - (double)lo * (double)lo);
+    double eh = fabs(xd - (double)hi * (double)hi);
+    float r = y;
+    if (el < ey) { r = lo; ey = el; }
+    if (eh < ey) r = hi;
+    return r;
+}
+
 }  // namespace wq

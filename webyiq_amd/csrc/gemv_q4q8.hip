@@ -30,6 +30,7 @@ namespace {
 struct GemvParams {
     LinearArgs a;
     ArgmaxArgs am;
+    QuantInArgs qin;  // QIN kernels: the f32 input and optional RMSNorm
     int J;       // passes per row = ceil(K / 2048)
     int nslots;  // row slots per workgroup = waves / J
     int RB;      // rows per workgroup = nslots * IPW
@@ -39,7 +40,7 @@ struct GemvParams {
     int nblocks; // gridDim.x
 };
 
-template <int MT, int MODE, int G, bool PT, int IPW, bool ARGMAX>
+template <int MT, int MODE, int G, bool PT, int IPW, bool ARGMAX, bool QIN>
 __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     constexpr int GE = PT ? G : 32;        // accumulation group
     constexpr int LPG = GE / 32;           // lanes per accumulation group (1 or 4)
@@ -55,6 +56,10 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     if (ARGMAX) {
         pin_arg(p.am.ids); pin_arg(p.am.tok_out); pin_arg(p.am.keys); pin_arg(p.am.ticket);
         pin_arg(p.nblocks);
+    }
+    if (QIN) {
+        pin_arg(p.qin.x); pin_arg(p.qin.norm_w); pin_arg(p.qin.eps);
+        pin_arg(p.qin.xq); pin_arg(p.qin.dx); pin_arg(p.qin.xs);
     }
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -76,6 +81,9 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     float2* sm_lds = reinterpret_cast<float2*>(acc_lds + (size_t)MT * NH * RB * NEP);
     float* xs_lds = reinterpret_cast<float*>(sm_lds + (size_t)NH * RB * NG);
     float* dx_lds = xs_lds + (size_t)MT * NE;
+    // fused quantiser scratch (QIN kernels have no argmax keys)
+    static_assert(!(QIN && ARGMAX), "no fused quantiser in the lm_head kernel");
+    float* qin_lds = dx_lds + (size_t)MT * NDX;
 
     // Lanes past the end of a partial pass (K % 2048 != 0) load from position 0
     // and never write their results: every load below is unconditional, so no
@@ -87,6 +95,25 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     const int g = kpos / G;   // this lane's weight group
     const size_t row_bytes = (size_t)K / 2;
     const unsigned char* wbase = reinterpret_cast<const unsigned char*>(a.wq) + (size_t)kpos / 2;
+
+    // 0. fused quantiser input first: this lane's 32-code slice of each token
+    //    (and of the norm weight), so that waiting for it does not wait for
+    //    the weight stream issued after it
+    constexpr int QT = QIN ? MT : 1;
+    float4 qx[QT][8], qw[8];
+    if constexpr (QIN) {
+        const float* nsrc = p.qin.norm_w ? p.qin.norm_w : p.qin.x;  // unconditional loads
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const int64_t tt = t < a.M ? t : a.M - 1;
+            const float4* x4 = reinterpret_cast<const float4*>(p.qin.x + tt * a.K + kpos);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) qx[t][u] = x4[u];
+        }
+        const float4* n4 = reinterpret_cast<const float4*>(nsrc + kpos);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) qw[u] = n4[u];
+    }
 
     // 1. issue every global load of this lane before the first one is consumed
     //    (one memory round trip; rows past N re-read row N-1)
@@ -105,14 +132,107 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     uint4 xa[MT], xb[MT];
     int32_t xsv[MT];
     float dxv[MT];
+    if constexpr (!QIN) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-        int64_t tt = t < a.M ? t : a.M - 1;
-        const unsigned char* xp = reinterpret_cast<const unsigned char*>(a.xq) + tt * a.K + kpos;
-        xa[t] = load16(xp);
-        xb[t] = load16(xp + 16);
-        xsv[t] = a.xs[tt * NE + e];
-        dxv[t] = a.dx[tt * NDX + (PT ? 0 : e)];
+        for (int t = 0; t < MT; ++t) {
+            int64_t tt = t < a.M ? t : a.M - 1;
+            const unsigned char* xp = reinterpret_cast<const unsigned char*>(a.xq) + tt * a.K + kpos;
+            xa[t] = load16(xp);
+            xb[t] = load16(xp + 16);
+            xsv[t] = a.xs[tt * NE + e];
+            dxv[t] = a.dx[tt * NDX + (PT ? 0 : e)];
+        }
+    } else {
+        // Fused per-token quantiser, while the weight loads are in flight:
+        // the quant_act kernel's arithmetic and reduction order, so codes,
+        // scales and sums are bit-identical to wq_quant_act's.  Every wave
+        // holds the slices of its pass j; the slot-0 waves cover the row once.
+        static_assert(!QIN || (PT && MT <= 2), "the fused quantiser is per token, M <= 2");
+        float* red = qin_lds;             // [MT][8] pass sums of squares
+        float* wmax = qin_lds + MT * 8;   // [MT][16] absmax partials per wave
+        if (p.qin.norm_w) {
+            // slice fmaf chain, wavefront xor butterfly, pass sums in pass order
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                float pp = 0.0f;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    pp = fmaf(qx[t][u].x, qx[t][u].x, pp);
+                    pp = fmaf(qx[t][u].y, qx[t][u].y, pp);
+                    pp = fmaf(qx[t][u].z, qx[t][u].z, pp);
+                    pp = fmaf(qx[t][u].w, qx[t][u].w, pp);
+                }
+                pp = kact ? pp : 0.0f;
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) pp = pp + __shfl_xor(pp, o);
+                if (slot == 0 && lane == 0) red[t * 8 + j] = pp;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                float total = 0.0f;
+                for (int jj = 0; jj < p.J; ++jj) total = total + red[t * 8 + jj];
+                const float r = 1.0f / sqrt_rn(total / (float)K + p.qin.eps);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    qx[t][u].x = (qx[t][u].x * r) * qw[u].x;
+                    qx[t][u].y = (qx[t][u].y * r) * qw[u].y;
+                    qx[t][u].z = (qx[t][u].z * r) * qw[u].z;
+                    qx[t][u].w = (qx[t][u].w * r) * qw[u].w;
+                }
+            }
+        }
+        // per-token absmax (order-free), dx = amax / 127
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            float mx = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(qx[t][u].x), fabsf(qx[t][u].y)),
+                                     fmaxf(fabsf(qx[t][u].z), fabsf(qx[t][u].w))));
+            mx = kact ? mx : 0.0f;
+            for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+            if (lane == 0) wmax[t * 16 + wave] = mx;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            float amax = wmax[t * 16];
+            for (int w = 1; w < NW; ++w) amax = fmaxf(amax, wmax[t * 16 + w]);
+            dxv[t] = amax / 127.0f;
+        }
+        // this lane's 32 codes and its group's code sum
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const int64_t tt = t < a.M ? t : a.M - 1;
+            const float d = dxv[t];
+            uint32_t wds[8];
+            int cs = 0;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+                if (d > 0.0f) {
+                    q0 = (int)rintf(qx[t][u].x / d);
+                    q1 = (int)rintf(qx[t][u].y / d);
+                    q2 = (int)rintf(qx[t][u].z / d);
+                    q3 = (int)rintf(qx[t][u].w / d);
+                }
+                wds[u] = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+                         ((uint32_t)(q3 & 0xFF) << 24);
+                cs += q0 + q1 + q2 + q3;
+            }
+            xa[t] = make_uint4(wds[0], wds[1], wds[2], wds[3]);
+            xb[t] = make_uint4(wds[4], wds[5], wds[6], wds[7]);
+            xsv[t] = LPG == 4 ? quad_sum(cs) : cs;
+            // workgroup 0 hands the quantised activations to later consumers
+            if (blockIdx.x == 0 && slot == 0 && kact && t < a.M) {
+                int8_t* xo = p.qin.xq + tt * a.K + kpos;
+                *reinterpret_cast<uint4*>(xo) = xa[t];
+                *reinterpret_cast<uint4*>(xo + 16) = xb[t];
+                if ((lane % LPG) == 0) p.qin.xs[tt * NE + e] = xsv[t];
+                if (tid == 0) p.qin.dx[tt] = d;
+            }
+        }
     }
 
     // 2. activation sums / scales and weight (s, m) -> LDS
@@ -310,7 +430,7 @@ constexpr int64_t kGemvTargetWgs = WQ_GEMV_TARGET_WGS;  // MI355X: 256 CUs
 
 int round_tokens(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
-Plan make_plan(const LinearArgs& a, bool argmax) {
+Plan make_plan(const LinearArgs& a, bool argmax, bool qin = false) {
     Plan p{};
     p.MT = round_tokens(a.M);
     const bool pt = a.GA == a.K;
@@ -336,6 +456,7 @@ Plan make_plan(const LinearArgs& a, bool argmax) {
         size_t b = (size_t)p.MT * nh * rb * p.NEP * 4 + (size_t)nh * rb * p.NG * 8 +
                    (size_t)p.MT * p.NE * 4 + (size_t)p.MT * (pt ? 1 : a.K / 32) * 4;
         if (argmax) b += 16 + (size_t)p.MT * rb * 8;
+        if (qin) b += (size_t)p.MT * (8 + 16) * 4;
         return b;
     };
     // registers: weights in flight (4 per row half) + activations (8 per token)
@@ -349,37 +470,47 @@ Plan make_plan(const LinearArgs& a, bool argmax) {
     return p;
 }
 
-template <int MT, int MODE, int G, bool PT, bool ARGMAX>
+template <int MT, int MODE, int G, bool PT, bool ARGMAX, bool QIN>
 hipError_t launch_ipw(const Plan& pl, const GemvParams& gp, hipStream_t s) {
     dim3 grid(pl.grid), block(64 * pl.waves);
     switch (pl.IPW) {
-        case 1: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 1, ARGMAX>), grid, block, pl.lds, s, gp); break;
-        case 2: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 2, ARGMAX>), grid, block, pl.lds, s, gp); break;
-        case 4: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 4, ARGMAX>), grid, block, pl.lds, s, gp); break;
-        case 6: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 6, ARGMAX>), grid, block, pl.lds, s, gp); break;
-        default: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 8, ARGMAX>), grid, block, pl.lds, s, gp); break;
+        case 1: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 1, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
+        case 2: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 2, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
+        case 4: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 4, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
+        case 6: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 6, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
+        default: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 8, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
     }
     return hipGetLastError();
 }
 
-template <int MT, int MODE, bool ARGMAX>
+template <int MT, int MODE, bool ARGMAX, bool QIN>
 hipError_t launch_gpt(const Plan& pl, const GemvParams& gp, hipStream_t s) {
     const bool pt = gp.a.GA == gp.a.K;
-    if (gp.a.G == 128) {
-        return pt ? launch_ipw<MT, MODE, 128, true, ARGMAX>(pl, gp, s)
-                  : launch_ipw<MT, MODE, 128, false, ARGMAX>(pl, gp, s);
+    if constexpr (QIN) {  // per token only (checked on the host)
+        return gp.a.G == 128 ? launch_ipw<MT, MODE, 128, true, ARGMAX, true>(pl, gp, s)
+                             : launch_ipw<MT, MODE, 32, true, ARGMAX, true>(pl, gp, s);
+    } else {
+        if (gp.a.G == 128) {
+            return pt ? launch_ipw<MT, MODE, 128, true, ARGMAX, false>(pl, gp, s)
+                      : launch_ipw<MT, MODE, 128, false, ARGMAX, false>(pl, gp, s);
+        }
+        return pt ? launch_ipw<MT, MODE, 32, true, ARGMAX, false>(pl, gp, s)
+                  : launch_ipw<MT, MODE, 32, false, ARGMAX, false>(pl, gp, s);
     }
-    return pt ? launch_ipw<MT, MODE, 32, true, ARGMAX>(pl, gp, s)
-              : launch_ipw<MT, MODE, 32, false, ARGMAX>(pl, gp, s);
 }
 
-template <int MODE, bool ARGMAX>
+template <int MODE, bool ARGMAX, bool QIN>
 hipError_t launch_mt(const Plan& pl, const GemvParams& gp, hipStream_t s) {
-    switch (pl.MT) {
-        case 1: return launch_gpt<1, MODE, ARGMAX>(pl, gp, s);
-        case 2: return launch_gpt<2, MODE, ARGMAX>(pl, gp, s);
-        case 4: return launch_gpt<4, MODE, ARGMAX>(pl, gp, s);
-        default: return launch_gpt<8, MODE, ARGMAX>(pl, gp, s);
+    if constexpr (QIN) {  // M <= 2 (checked on the host)
+        return pl.MT == 1 ? launch_gpt<1, MODE, ARGMAX, true>(pl, gp, s)
+                          : launch_gpt<2, MODE, ARGMAX, true>(pl, gp, s);
+    } else {
+        switch (pl.MT) {
+            case 1: return launch_gpt<1, MODE, ARGMAX, false>(pl, gp, s);
+            case 2: return launch_gpt<2, MODE, ARGMAX, false>(pl, gp, s);
+            case 4: return launch_gpt<4, MODE, ARGMAX, false>(pl, gp, s);
+            default: return launch_gpt<8, MODE, ARGMAX, false>(pl, gp, s);
+        }
     }
 }
 
@@ -402,9 +533,9 @@ hipError_t launch_gemv(const LinearArgs& a, hipStream_t s) {
     Plan pl = make_plan(a, false);
     GemvParams gp = params_of(a, pl);
     switch (a.mode) {
-        case 0: return launch_mt<0, false>(pl, gp, s);
-        case 1: return launch_mt<1, false>(pl, gp, s);
-        default: return launch_mt<2, false>(pl, gp, s);
+        case 0: return launch_mt<0, false, false>(pl, gp, s);
+        case 1: return launch_mt<1, false, false>(pl, gp, s);
+        default: return launch_mt<2, false, false>(pl, gp, s);
     }
 }
 
@@ -412,7 +543,18 @@ hipError_t launch_lm_head_argmax(const LinearArgs& a, const ArgmaxArgs& am, hipS
     Plan pl = make_plan(a, true);
     GemvParams gp = params_of(a, pl);
     gp.am = am;
-    return launch_mt<0, true>(pl, gp, s);
+    return launch_mt<0, true, false>(pl, gp, s);
+}
+
+hipError_t launch_gemv_quant_in(const LinearArgs& a, const QuantInArgs& q, hipStream_t s) {
+    Plan pl = make_plan(a, false, true);
+    GemvParams gp = params_of(a, pl);
+    gp.qin = q;
+    switch (a.mode) {
+        case 0: return launch_mt<0, false, true>(pl, gp, s);
+        case 1: return launch_mt<1, false, true>(pl, gp, s);
+        default: return launch_mt<2, false, true>(pl, gp, s);
+    }
 }
 
 }  // namespace wq

@@ -40,6 +40,16 @@ struct ArgmaxArgs {
     unsigned int* ticket;      // workspace: [kArgmaxSlots] slot counters + 1 top counter, one line each
 };
 
+// Input of a GEMV that quantises its own activations (per token).
+struct QuantInArgs {
+    const float* x;       // [M, K] f32
+    const float* norm_w;  // nullable: RMSNorm prologue when set
+    float eps;
+    int8_t* xq;           // nullable outputs: the quantised activations
+    float* dx;            //   (xq [M, K], dx [M], xs [M, K/G])
+    int32_t* xs;
+};
+
 struct EmbedArgs {
     const uint32_t* q;    // [V, K/8] packed int4 rows
     const uint32_t* s;    // [V, K/G] (scale, min) words
@@ -65,6 +75,7 @@ hipError_t launch_quant_act(const QuantArgs& a, hipStream_t s);
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t s);
 hipError_t launch_gather_rows(const GatherArgs& a, hipStream_t s);
 hipError_t launch_gemv(const LinearArgs& a, hipStream_t s);
+hipError_t launch_gemv_quant_in(const LinearArgs& a, const QuantInArgs& q, hipStream_t s);
 hipError_t launch_lm_head_argmax(const LinearArgs& a, const ArgmaxArgs& am, hipStream_t s);
 hipError_t launch_gemm(const LinearArgs& a, hipStream_t s);
 hipError_t launch_argmax(const float* logits, int64_t M, int64_t V, const uint32_t* ids,

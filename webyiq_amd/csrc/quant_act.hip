@@ -1,14 +1,9 @@
-// Activation quantiser (webyIQ crates/engine/src/shaders/quant.wgsl:19-62 and
-// the torch fake-quant hook tools/reference.py:43-48), one workgroup per token.
-//
-//   optional RMSNorm: v = (x * r) * nw, r = 1 / sqrt(mean(x^2) + eps)
-//   per activation group (GA = K or 32): dx = amax / 127,
-//   xq = dx > 0 ? round_half_even(v / dx) : 0   (IEEE division, as torch)
-//   xs[e] = sum of xq over accumulation group e (Ge = min(G, GA) elements)
-//
-// Thread i of the 256 owns float4 chunks i, i+256, ...; every reduction that
-// feeds a rounding (the RMSNorm sum of squares) runs in a fixed order that the
-// CPU oracle restates, so int8 codes are reproducible bit for bit.
+// Lane l of wave w owns the 32-element slices 2048 j + 32 l of the passes
+// j = w, w + 4, ... of its token's row -- the slice a decode GEMV lane owns --
+// and every reduction that feeds a rounding (the RMSNorm sum of squares) runs
+// in a fixed order the CPU oracle restates: an fmaf chain per slice, a
+// wavefront xor butterfly per pass, pass sums added in pass order.  So int8
+// codes are reproducible bit for bit, here and in the fused GEMV quantiser.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -18,144 +13,163 @@ namespace wq {
 namespace {
 
 constexpr int kQuantThreads = 256;
+constexpr int kQuantWaves = kQuantThreads / 64;
+constexpr int kPass = 2048;  // codes per wavefront pass (64 lanes x 32)
 
-// Correctly rounded single-precision square root: the hardware estimate is
-// within one ulp, and the candidate with the smallest |x - c^2| (exact in
-// double: c^2 has 48 significant bits) is the rounded root (a square root is
-// never exactly halfway between two floats).
-__device__ float sqrt_rn(float x) {
-    float y = __builtin_amdgcn_sqrtf(x);
-    if (!(x > 0.0f) || isinf(x) || !(y > 0.0f)) return y;
-    float lo = __uint_as_float(__float_as_uint(y) - 1u);
-    float hi = __uint_as_float(__float_as_uint(y) + 1u);
-    double xd = (double)x;
-    double ey = fabs(xd - (double)y * (double)y);
-    double el = fabs(xd - (double)lo * (double)lo);
-    double eh = fabs(xd - (double)hi * (double)hi);
-    float r = y;
-    if (el < ey) { r = lo; ey = el; }
-    if (eh < ey) r = hi;
-    return r;
-}
-
-// Up to kCacheChunks float4 per thread stay in registers (K <= 8192): the row
-// is read from memory once; longer rows are re-read (L2 hits) per pass.
-constexpr int kCacheChunks = 8;
-
+// CACHED (K <= 4 passes): one slice per lane, loaded once and kept in
+// registers.  Longer rows are re-read (L2 hits) in each phase.
 template <bool NORM, bool PER_TOKEN, int GE, bool CACHED>
 __global__ __launch_bounds__(kQuantThreads) void quant_act_kernel(QuantArgs a) {
     pin_arg(a.x); pin_arg(a.norm_w); pin_arg(a.eps); pin_arg(a.K);
     pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
     const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
     const int64_t t = blockIdx.x;
     const int K = (int)a.K;
-    const int nchunk = K / 4;
-    const int jmax = (nchunk + kQuantThreads - 1) / kQuantThreads;
-    const int JL = CACHED ? kCacheChunks : jmax;  // constant trip count when cached
-    const float4* xr = reinterpret_cast<const float4*>(a.x + t * a.K);
-    const float4* nw = reinterpret_cast<const float4*>(a.norm_w);
-    __shared__ float red[kQuantThreads];
-    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int J = (K + kPass - 1) / kPass;
+    const int NL = CACHED ? 1 : (J - wave + kQuantWaves - 1) / kQuantWaves;  // this wave's passes
+    const float* xr = a.x + t * a.K;
+    __shared__ float red[kQuantWaves];
 
-    // one round of loads: the whole row (and norm weight) for this thread
-    float4 xc[CACHED ? kCacheChunks : 1], wc[CACHED && NORM ? kCacheChunks : 1];
-    if (CACHED) {
+    // slice i of this lane: pass j = wave + 4 i, codes [base, base + 32)
+    auto base_of = [&](int i) { return kPass * (wave + kQuantWaves * i) + 32 * lane; };
+    auto load_slice = [&](int b, float4* v) {
+        const float4* p = reinterpret_cast<const float4*>(xr + b);
 #pragma unroll
-        for (int j = 0; j < kCacheChunks; ++j) {
-            int c = tid + kQuantThreads * j;
-            bool ok = j < jmax && c < nchunk;
-            xc[j] = ok ? xr[c] : zero4;
-            if (NORM) wc[j] = ok ? nw[c] : zero4;
+        for (int u = 0; u < 8; ++u) v[u] = p[u];
+    };
+    float4 xc[8], wc[8];
+    const bool act0 = base_of(0) < K && wave < J;
+    if (CACHED) {
+        load_slice(act0 ? base_of(0) : 0, xc);
+        if (NORM) {
+            const float4* p = reinterpret_cast<const float4*>(a.norm_w + (act0 ? base_of(0) : 0));
+#pragma unroll
+            for (int u = 0; u < 8; ++u) wc[u] = p[u];
         }
     }
-    auto raw = [&](int j, int c) -> float4 { return CACHED ? xc[CACHED ? j : 0] : xr[c]; };
-
+    // this lane's slice i as (optionally normalised) values
     float r = 1.0f;
-    if (NORM) {
-        float p = 0.0f;
+    auto slice = [&](int i, float4* v) {
+        const int b = base_of(i);
+        if (CACHED) {
 #pragma unroll
-        for (int j = 0; j < JL; ++j) {
-            int c = tid + kQuantThreads * j;
-            if (j < jmax && c < nchunk) {
-                float4 v = raw(j, c);
-                p = fmaf(v.x, v.x, p);
-                p = fmaf(v.y, v.y, p);
-                p = fmaf(v.z, v.z, p);
-                p = fmaf(v.w, v.w, p);
+            for (int u = 0; u < 8; ++u) v[u] = xc[u];
+        } else {
+            load_slice(b, v);
+        }
+        if (NORM) {
+            const float4* p = reinterpret_cast<const float4*>(a.norm_w + b);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float4 w = CACHED ? wc[u] : p[u];
+                v[u].x = (v[u].x * r) * w.x;
+                v[u].y = (v[u].y * r) * w.y;
+                v[u].z = (v[u].z * r) * w.z;
+                v[u].w = (v[u].w * r) * w.w;
             }
         }
-        red[tid] = p;
-        __syncthreads();
-        for (int s = kQuantThreads / 2; s > 0; s >>= 1) {
-            if (tid < s) red[tid] = red[tid] + red[tid + s];
+    };
+
+    if (NORM) {
+        // rounds of 4 passes: wave w adds pass 4 q + w; every thread then adds
+        // the round's pass sums in pass order
+        float total = 0.0f;
+        const int rounds = (J + kQuantWaves - 1) / kQuantWaves;
+        for (int q = 0; q < rounds; ++q) {
+            const int b = kPass * (wave + kQuantWaves * q) + 32 * lane;
+            float pp = 0.0f;
+            if (wave + kQuantWaves * q < J && b < K) {
+                float4 v[8];
+                if (CACHED) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) v[u] = xc[u];
+                } else {
+                    load_slice(b, v);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    pp = fmaf(v[u].x, v[u].x, pp);
+                    pp = fmaf(v[u].y, v[u].y, pp);
+                    pp = fmaf(v[u].z, v[u].z, pp);
+                    pp = fmaf(v[u].w, v[u].w, pp);
+                }
+            }
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) pp = pp + __shfl_xor(pp, o);
+            if (lane == 0) red[wave] = pp;
+            __syncthreads();
+            const int np = min(kQuantWaves, J - kQuantWaves * q);
+            for (int w = 0; w < np; ++w) total = total + red[w];
             __syncthreads();
         }
-        r = 1.0f / sqrt_rn(red[0] / (float)K + a.eps);
-        __syncthreads();
+        r = 1.0f / sqrt_rn(total / (float)K + a.eps);
     }
-
-    auto load = [&](int j, int c) -> float4 {
-        float4 v = raw(j, c);
-        if (NORM) {
-            float4 w = CACHED ? wc[CACHED && NORM ? j : 0] : nw[c];
-            v.x = (v.x * r) * w.x;
-            v.y = (v.y * r) * w.y;
-            v.z = (v.z * r) * w.z;
-            v.w = (v.w * r) * w.w;
-        }
-        return v;
-    };
 
     // Per-token scale: block-wide absolute maximum (exact, order-free).
     float dtok = 0.0f;
     if (PER_TOKEN) {
         float m = 0.0f;
+        for (int i = 0; i < NL; ++i) {
+            if (base_of(i) >= K || (CACHED && !act0)) continue;
+            float4 v[8];
+            slice(i, v);
 #pragma unroll
-        for (int j = 0; j < JL; ++j) {
-            int c = tid + kQuantThreads * j;
-            if (j < jmax && c < nchunk) {
-                float4 v = load(j, c);
-                m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-            }
+            for (int u = 0; u < 8; ++u)
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
         }
         for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        if ((tid & 63) == 0) red[tid >> 6] = m;
+        if (lane == 0) red[wave] = m;
         __syncthreads();
         float amax = red[0];
-        for (int w = 1; w < kQuantThreads / 64; ++w) amax = fmaxf(amax, red[w]);
+        for (int w = 1; w < kQuantWaves; ++w) amax = fmaxf(amax, red[w]);
         dtok = amax / 127.0f;
         if (tid == 0) a.dx[t] = dtok;
     }
 
-    uint32_t* xq = reinterpret_cast<uint32_t*>(a.xq + t * a.K);
-    constexpr int kLanesPerGe = GE / 4;  // lanes (float4 chunks) per xs group
+    for (int i = 0; i < NL; ++i) {
+        const int b = base_of(i);
+        const bool valid = b < K && (!CACHED || act0);
+        float4 v[8];
+        if (valid) {
+            slice(i, v);
+        } else {
 #pragma unroll
-    for (int j = 0; j < JL; ++j) {
-        if (j >= jmax) break;
-        int c = tid + kQuantThreads * j;
-        bool valid = c < nchunk;
-        float4 v = valid ? load(j, c) : zero4;
+            for (int u = 0; u < 8; ++u) v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
         float d = dtok;
         if (!PER_TOKEN) {
-            // 32-element activation group = 8 consecutive lanes
-            float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-            for (int o = 1; o < 8; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+            // the slice is one 32-element activation group
+            float m = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
             d = m / 127.0f;
-            if (valid && (tid & 7) == 0) a.dx[t * (a.K / 32) + c / 8] = d;
+            if (valid) a.dx[t * (a.K / 32) + b / 32] = d;
         }
-        int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
-        if (d > 0.0f) {
-            q0 = (int)rintf(v.x / d);
-            q1 = (int)rintf(v.y / d);
-            q2 = (int)rintf(v.z / d);
-            q3 = (int)rintf(v.w / d);
+        uint32_t wds[8];
+        int cs = 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+            if (d > 0.0f) {
+                q0 = (int)rintf(v[u].x / d);
+                q1 = (int)rintf(v[u].y / d);
+                q2 = (int)rintf(v[u].z / d);
+                q3 = (int)rintf(v[u].w / d);
+            }
+            wds[u] = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+                     ((uint32_t)(q3 & 0xFF) << 24);
+            cs += q0 + q1 + q2 + q3;
         }
-        if (valid)
-            xq[c] = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) |
-                    ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)(q3 & 0xFF) << 24);
-        int s = q0 + q1 + q2 + q3;
-        for (int o = 1; o < kLanesPerGe; o <<= 1) s += __shfl_xor(s, o);
-        if (valid && (tid % kLanesPerGe) == 0) a.xs[t * (a.K / GE) + c / kLanesPerGe] = s;
+        if (GE == 128) cs = quad_sum(cs);  // 4 consecutive lanes = one 128-group
+        if (valid) {
+            uint4* xo = reinterpret_cast<uint4*>(a.xq + t * a.K + b);
+            xo[0] = make_uint4(wds[0], wds[1], wds[2], wds[3]);
+            xo[1] = make_uint4(wds[4], wds[5], wds[6], wds[7]);
+            if ((lane % (GE / 32)) == 0) a.xs[t * (a.K / GE) + b / GE] = cs;
+        }
     }
 }
 
@@ -176,7 +190,7 @@ hipError_t dispatch_quant(const QuantArgs& a, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_quant_act(const QuantArgs& a, hipStream_t s) {
-    const bool cached = a.K <= 4 * kQuantThreads * kCacheChunks;
+    const bool cached = a.K <= kQuantWaves * kPass;
     if (a.norm_w) return cached ? dispatch_quant<true, true>(a, s) : dispatch_quant<true, false>(a, s);
     return cached ? dispatch_quant<false, true>(a, s) : dispatch_quant<false, false>(a, s);
 }

@@ -130,6 +130,24 @@ def gemv(w: Q4Tensor, a: Acts, mode=MODE_STORE, y=None, stream=None):
     return _linear("wq_gemv", w, a, mode, y, stream)
 
 
+def quant_gemv(w: Q4Tensor, x, norm=None, eps=1e-6, mode=MODE_STORE, y=None, out: Optional[Acts] = None,
+               stream=None):
+    """quant (per token) then gemv, M <= 8, in one launch for M <= 2; returns
+    (y, the quantised activations) -- the norm_quant -> matmul pairs of the
+    decode layer (graph.rs:266-269, 323-326)."""
+    if x.dim() == 1:
+        x = x[None]
+    M, K = x.shape
+    a = out if out is not None else empty_acts(M, K, None, w.G, x.device)
+    if a.GA != K or a.G != w.G:
+        raise ValueError("quant_gemv writes per-token activations for the weight's group")
+    N = _nrows(w, mode)
+    y = _out(y, M, N, x.device, mode)
+    _lib.call("wq_quant_gemv", _stream(stream), _ptr(x), _ptr(norm), float(eps), _ptr(w.q), _ptr(w.s), N,
+              w.K, w.G, M, mode, _ptr(a.xq), _ptr(a.dx), _ptr(a.xs), _ptr(y))
+    return y, a
+
+
 def gemm(w: Q4Tensor, a: Acts, mode=MODE_STORE, y=None, stream=None):
     """Prefill GEMM on int8 MFMA (Builder::gemm, gemm_q4q8.wgsl)."""
     return _linear("wq_gemm", w, a, mode, y, stream)
