@@ -149,23 +149,30 @@ void or_q4_quantize(const float* w, int64_t N, int64_t K, int G,
 
 /* --------------------------------------------------- activation quant ---- */
 
-/* RMSNorm prologue in the kernels' reduction order.  The row is cut into
- * 32-element slices (one GPU lane each); a slice's partial is an fmaf chain
- * over its elements in index order.  The 64 slices of each 2048-element pass
- * (one wavefront) are combined by a pairwise tree with offsets 1, 2, ..., 32
- * (p[i] += p[i + o] for i with bit o clear: the wavefront's xor butterfly),
- * slices past K counting as 0; the pass sums are then added in pass order.
+/* RMSNorm prologue in the kernels' reduction order.  The row is read in
+ * passes of 2048 elements: in load u (0..7) of pass j, lane l (0..63) holds
+ * the float4 chunk 512 j + 64 u + l (coalesced).  Chunk u's partial c_u is
+ * an fmaf chain over its 4 elements in index order; a lane's partial is the
+ * pairwise tree ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), so that
+ * waves holding 2, 4 or 8 of the loads can form it together.  The 64 lane
+ * partials of a pass are combined by a pairwise tree with offsets 1, 2, ...,
+ * 32 (p[i] += p[i + o] for i with bit o clear: the wavefront's xor
+ * butterfly); chunks past K count as 0; the pass sums are added in pass
+ * order.
  * quant.wgsl:24-39: r = 1/sqrt(mean(x^2) + eps); v = (x * r) * nw. */
 static float rms_scale(const float* x, int64_t K, float eps) {
     float total = 0.0f;
     for (int64_t j = 0; 2048 * j < K; ++j) {
         float p[64];
         for (int l = 0; l < 64; ++l) {
-            const int64_t b = 2048 * j + 32 * l;
-            float acc = 0.0f;
-            if (b < K)
-                for (int i = 0; i < 32; ++i) acc = fmaf(x[b + i], x[b + i], acc);
-            p[l] = acc;
+            float c[8];
+            for (int u = 0; u < 8; ++u) {
+                const int64_t b = 4 * (512 * j + 64 * u + l);
+                c[u] = 0.0f;
+                if (b < K)
+                    for (int e = 0; e < 4; ++e) c[u] = fmaf(x[b + e], x[b + e], c[u]);
+            }
+            p[l] = ((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]));
         }
         for (int o = 1; o < 64; o <<= 1)
             for (int i = 0; i < 64; ++i)

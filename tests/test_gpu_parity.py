@@ -83,6 +83,51 @@ def test_quant_zero_rows_and_ties():
         assert np.array_equal(host(a.xs), xs)
 
 
+def _half_boundary_rows(K):
+    """Rows whose every 32-group starts with the row's absmax (so per-token
+    and per-32 scales agree), followed by values within 3 ulps of the
+    half-integer code boundaries (k + 0.5) * d: ties, and the cases where a
+    quotient computed without a division would round the other way."""
+    rows = []
+    for amax in (np.float32(127.0), np.float32(3.7), np.float32(1e-3)):
+        d = np.float32(amax / np.float32(127.0))
+        vals = []
+        for k in range(-127, 127):
+            h = np.float32((np.float32(k) + np.float32(0.5)) * d)
+            for j in range(-3, 4):
+                v = h
+                for _ in range(abs(j)):
+                    v = np.nextafter(v, np.float32(np.inf if j > 0 else -np.inf), dtype=np.float32)
+                if abs(v) <= amax:
+                    vals.append(v)
+        vals = np.array(vals, np.float32)
+        row = np.resize(vals, (K // 32, 31))
+        row = np.concatenate([np.full((K // 32, 1), amax, np.float32), row], 1).reshape(K)
+        rows.append(row)
+    return np.stack(rows)
+
+
+def test_quant_half_boundaries():
+    """Codes at and around the rounding boundaries, bit-exact against the
+    oracle's IEEE division: quant_act (per token and per 32) and the fused
+    quantiser of wq_quant_gemv."""
+    note("quant half-integer boundaries")
+    K, N = 2048, 256
+    x = _half_boundary_rows(K)
+    for GA in (None, 32):
+        xq, dx, xs = orc.quant_act(x, GA, 128)
+        a = ops.quant(dev(x), GA=GA, G=128)
+        assert np.array_equal(host(a.xq), xq)
+        assert np.array_equal(host(a.xs), xs)
+    rng = np.random.default_rng(5)
+    wq, ws = ref.make_weight(rng, N, K, 128)
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, 128)
+    xq, dx, xs = orc.quant_act(x[:2], None, 128)
+    y, a = ops.quant_gemv(w, dev(x[:2]))
+    assert np.array_equal(host(a.xq), xq)
+    assert np.array_equal(host(y).view(np.uint32), orc.linear(wq, ws, K, 128, xq, dx, xs).view(np.uint32))
+
+
 # ------------------------------------------------------------------ GEMV ----
 
 GEMV_CASES = [

@@ -14,6 +14,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "quant_code.hpp"
+
 namespace wq {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -55,6 +57,83 @@ __device__ __forceinline__ int quad_sum(int v) {
     v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);  // quad_perm [1,0,3,2]
     v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);  // quad_perm [2,3,0,1]
     return v;
+}
+
+// DPP lane moves (gfx9 encodings).  Within a row of 16 lanes: quad_perm
+// [1,0,3,2] / [2,3,0,1] pair lanes i ^ 1 / i ^ 2; row_half_mirror pairs
+// i with 7 - i in each half-row, row_mirror i with 15 - i.  row_bcast15 /
+// row_bcast31 hand lane 15 (31) to the next row (rows 2 and 3).
+constexpr int kDppXor1 = 0xB1;
+constexpr int kDppXor2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+constexpr int kDppBcast15 = 0x142;
+constexpr int kDppBcast31 = 0x143;
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, false);
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Sum of the 64 lanes in the order of the xor butterfly (p[i] + p[i ^ o] for
+// o = 1, 2, ..., 32: a pairwise tree in lane order), returned to every lane.
+// After each level the partners' values are equal, so the mirror moves pair
+// the same values as the xor partners and each addition is one of the
+// tree's (IEEE addition commutes).  Rows 1 and 3 form R0 + R1 and R2 + R3;
+// row 3 then adds R0 + R1.
+__device__ __forceinline__ float wave_sum_tree(float v) {
+    v = v + dpp_f<kDppXor1>(v);
+    v = v + dpp_f<kDppXor2>(v);
+    v = v + dpp_f<kDppHalfMirror>(v);
+    v = v + dpp_f<kDppMirror>(v);
+    v = v + dpp_f<kDppBcast15, 0xA>(v);  // rows 0, 2 add +0 (unused)
+    v = v + dpp_f<kDppBcast31, 0xC>(v);  // row 3: (R2 + R3) + (R0 + R1)
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Sum of squares of one float4 chunk: an fmaf chain in index order.
+__device__ __forceinline__ float chunk_ss(float4 v) {
+    float c = fmaf(v.x, v.x, 0.0f);
+    c = fmaf(v.y, v.y, c);
+    c = fmaf(v.z, v.z, c);
+    return fmaf(v.w, v.w, c);
+}
+
+// Maximum of the 64 lanes (exact, order-free), returned to every lane.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kDppMirror>(v));
+    v = fmaxf(v, dpp_f<kDppBcast15, 0xA>(v));
+    v = fmaxf(v, dpp_f<kDppBcast31, 0xC>(v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Maximum over aligned groups of 8 lanes, in every lane of the group
+// (|values| >= 0, so the 0 that a masked move never produces is harmless).
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    return fmaxf(v, dpp_f<kDppHalfMirror>(v));
+}
+
+// Exact int32 sums over aligned groups of 8 lanes (every lane of the group)
+// and of 32 lanes (in rows 1 and 3: lanes 16..31 hold lanes 0..31's sum,
+// lanes 48..63 that of lanes 32..63).
+__device__ __forceinline__ int sum8(int v) {
+    v += dpp_i<kDppXor1>(v);
+    v += dpp_i<kDppXor2>(v);
+    return v + dpp_i<kDppHalfMirror>(v);
+}
+__device__ __forceinline__ int sum32_rows13(int v) {
+    v = sum8(v);
+    v += dpp_i<kDppMirror>(v);
+    return v + dpp_i<kDppBcast15, 0xA>(v);
 }
 
 // Non-temporal 16-byte load for weights that are streamed exactly once.

@@ -96,23 +96,33 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     const size_t row_bytes = (size_t)K / 2;
     const unsigned char* wbase = reinterpret_cast<const unsigned char*>(a.wq) + (size_t)kpos / 2;
 
-    // 0. fused quantiser input first: this lane's 32-code slice of each token
-    //    (and of the norm weight), so that waiting for it does not wait for
-    //    the weight stream issued after it
+    // 0. fused quantiser input first, coalesced and split between the
+    //    nslots waves of a pass: the wave of pass j and slot s reads loads
+    //    u0 + i (u0 = s * us, i < us = 8 / nslots), i.e. chunks
+    //    512 j + 64 u + lane, of each token and of the norm weight.  Issued
+    //    before the weight stream, so waiting for them does not wait for it.
     constexpr int QT = QIN ? MT : 1;
     float4 qx[QT][8], qw[8];
+    const int qus = 8 / p.nslots, qu0 = slot * qus;
     if constexpr (QIN) {
+        const int nchunk = K / 4;
         const float* nsrc = p.qin.norm_w ? p.qin.norm_w : p.qin.x;  // unconditional loads
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const int64_t tt = t < a.M ? t : a.M - 1;
-            const float4* x4 = reinterpret_cast<const float4*>(p.qin.x + tt * a.K + kpos);
+        for (int i = 0; i < 8; ++i) {
+            if (i < qus) {
+                const int c = 512 * j + 64 * (qu0 + i) + lane;
+                const int cc = c < nchunk ? c : 0;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) qx[t][u] = x4[u];
+                for (int t = 0; t < MT; ++t) {
+                    const int64_t tt = t < a.M ? t : a.M - 1;
+                    qx[t][i] = reinterpret_cast<const float4*>(p.qin.x + tt * a.K)[cc];
+                }
+                qw[i] = reinterpret_cast<const float4*>(nsrc)[cc];
+            }
         }
-        const float4* n4 = reinterpret_cast<const float4*>(nsrc + kpos);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) qw[u] = n4[u];
+        // keep these loads ahead of the weight stream (no sinking into their
+        // use, which would wait for every weight load)
+        asm volatile("" ::: "memory");
     }
 
     // 1. issue every global load of this lane before the first one is consumed
@@ -144,28 +154,44 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         }
     } else {
         // Fused per-token quantiser, while the weight loads are in flight:
-        // the quant_act kernel's arithmetic and reduction order, so codes,
-        // scales and sums are bit-identical to wq_quant_act's.  Every wave
-        // holds the slices of its pass j; the slot-0 waves cover the row once.
+        // the quant_act kernels' arithmetic and reduction order (per-chunk
+        // fmaf chains, a pairwise tree over a lane's 8 chunks -- here split
+        // over the waves of the pass and completed through LDS -- a pairwise
+        // tree over the lanes, pass sums in pass order), so codes, scales and
+        // sums are bit-identical to wq_quant_act's.  Each wave quantises its
+        // own chunks into LDS; every wave then reads its lane's 32 codes.
         static_assert(!QIN || (PT && MT <= 2), "the fused quantiser is per token, M <= 2");
-        float* red = qin_lds;             // [MT][8] pass sums of squares
-        float* wmax = qin_lds + MT * 8;   // [MT][16] absmax partials per wave
+        float* red = qin_lds;                 // [MT][8] pass sums of squares
+        float* wmax = qin_lds + MT * 8;       // [MT][8] absmax per wave
+        float* sub = qin_lds + MT * 16;       // [MT][8 waves][64] lane subtrees
+        uint32_t* codes = reinterpret_cast<uint32_t*>(  // [MT][K/4], 16-byte aligned
+            (reinterpret_cast<uintptr_t>(sub + MT * 8 * 64) + 15) & ~uintptr_t(15));
+        const int nchunk = K / 4;
+        const int nsl = p.nslots;
+        auto valid = [&](int i) { return i < qus && 512 * j + 64 * (qu0 + i) + lane < nchunk; };
         if (p.qin.norm_w) {
-            // slice fmaf chain, wavefront xor butterfly, pass sums in pass order
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
-                float pp = 0.0f;
+                float c[8];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    pp = fmaf(qx[t][u].x, qx[t][u].x, pp);
-                    pp = fmaf(qx[t][u].y, qx[t][u].y, pp);
-                    pp = fmaf(qx[t][u].z, qx[t][u].z, pp);
-                    pp = fmaf(qx[t][u].w, qx[t][u].w, pp);
+                for (int i = 0; i < 8; ++i) c[i] = valid(i) ? chunk_ss(qx[t][i]) : 0.0f;
+                // this wave's subtree: 2, 4 or 8 of the lane's chunks
+                float st = c[0] + c[1];
+                if (qus >= 4) st = st + (c[2] + c[3]);
+                if (qus == 8) st = st + ((c[4] + c[5]) + (c[6] + c[7]));
+                sub[(t * 8 + wave) * 64 + lane] = st;
+            }
+            __syncthreads();
+            if (slot == 0) {
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    const float* sp = sub + (t * 8 + j) * 64 + lane;  // slot s at wave s * J + j
+                    float pl = sp[0];
+                    if (nsl == 2) pl = pl + sp[p.J * 64];
+                    if (nsl == 4) pl = (pl + sp[64]) + (sp[128] + sp[192]);  // J == 1
+                    pl = wave_sum_tree(pl);
+                    if (lane == 0) red[t * 8 + j] = pl;
                 }
-                pp = kact ? pp : 0.0f;
-#pragma unroll
-                for (int o = 1; o < 64; o <<= 1) pp = pp + __shfl_xor(pp, o);
-                if (slot == 0 && lane == 0) red[t * 8 + j] = pp;
             }
             __syncthreads();
 #pragma unroll
@@ -174,11 +200,13 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
                 for (int jj = 0; jj < p.J; ++jj) total = total + red[t * 8 + jj];
                 const float r = 1.0f / sqrt_rn(total / (float)K + p.qin.eps);
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    qx[t][u].x = (qx[t][u].x * r) * qw[u].x;
-                    qx[t][u].y = (qx[t][u].y * r) * qw[u].y;
-                    qx[t][u].z = (qx[t][u].z * r) * qw[u].z;
-                    qx[t][u].w = (qx[t][u].w * r) * qw[u].w;
+                for (int i = 0; i < 8; ++i) {
+                    if (i < qus) {
+                        qx[t][i].x = (qx[t][i].x * r) * qw[i].x;
+                        qx[t][i].y = (qx[t][i].y * r) * qw[i].y;
+                        qx[t][i].z = (qx[t][i].z * r) * qw[i].z;
+                        qx[t][i].w = (qx[t][i].w * r) * qw[i].w;
+                    }
                 }
             }
         }
@@ -187,50 +215,62 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         for (int t = 0; t < MT; ++t) {
             float mx = 0.0f;
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(qx[t][u].x), fabsf(qx[t][u].y)),
-                                     fmaxf(fabsf(qx[t][u].z), fabsf(qx[t][u].w))));
-            mx = kact ? mx : 0.0f;
-            for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-            if (lane == 0) wmax[t * 16 + wave] = mx;
+            for (int i = 0; i < 8; ++i)
+                if (valid(i))
+                    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(qx[t][i].x), fabsf(qx[t][i].y)),
+                                         fmaxf(fabsf(qx[t][i].z), fabsf(qx[t][i].w))));
+            mx = wave_max(mx);
+            if (lane == 0) wmax[t * 8 + wave] = mx;
         }
         __syncthreads();
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-            float amax = wmax[t * 16];
-            for (int w = 1; w < NW; ++w) amax = fmaxf(amax, wmax[t * 16 + w]);
+            float amax = wmax[t * 8];
+            for (int w = 1; w < NW; ++w) amax = fmaxf(amax, wmax[t * 8 + w]);
             dxv[t] = amax / 127.0f;
         }
+        // codes of this wave's chunks -> LDS (and, from workgroup 0, to memory)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const float d = dxv[t], rd = 1.0f / d;
+            const int64_t tt = t < a.M ? t : a.M - 1;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (!valid(i)) continue;
+                const int c = 512 * j + 64 * (qu0 + i) + lane;
+                int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+                if (d > 0.0f) {
+                    q0 = quant_code(qx[t][i].x, d, rd);
+                    q1 = quant_code(qx[t][i].y, d, rd);
+                    q2 = quant_code(qx[t][i].z, d, rd);
+                    q3 = quant_code(qx[t][i].w, d, rd);
+                }
+                const uint32_t wd = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) |
+                                    ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)(q3 & 0xFF) << 24);
+                codes[t * nchunk + c] = wd;
+                if (blockIdx.x == 0 && t < a.M) reinterpret_cast<uint32_t*>(p.qin.xq + tt * a.K)[c] = wd;
+            }
+        }
+        __syncthreads();
         // this lane's 32 codes and its group's code sum
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-            const int64_t tt = t < a.M ? t : a.M - 1;
-            const float d = dxv[t];
-            uint32_t wds[8];
+            const uint4* cp = reinterpret_cast<const uint4*>(codes + t * nchunk + kpos / 4);
+            xa[t] = cp[0];
+            xb[t] = cp[1];
             int cs = 0;
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
-                if (d > 0.0f) {
-                    q0 = (int)rintf(qx[t][u].x / d);
-                    q1 = (int)rintf(qx[t][u].y / d);
-                    q2 = (int)rintf(qx[t][u].z / d);
-                    q3 = (int)rintf(qx[t][u].w / d);
-                }
-                wds[u] = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
-                         ((uint32_t)(q3 & 0xFF) << 24);
-                cs += q0 + q1 + q2 + q3;
-            }
-            xa[t] = make_uint4(wds[0], wds[1], wds[2], wds[3]);
-            xb[t] = make_uint4(wds[4], wds[5], wds[6], wds[7]);
+            cs = dot4(xa[t].x, 0x01010101u, cs);
+            cs = dot4(xa[t].y, 0x01010101u, cs);
+            cs = dot4(xa[t].z, 0x01010101u, cs);
+            cs = dot4(xa[t].w, 0x01010101u, cs);
+            cs = dot4(xb[t].x, 0x01010101u, cs);
+            cs = dot4(xb[t].y, 0x01010101u, cs);
+            cs = dot4(xb[t].z, 0x01010101u, cs);
+            cs = dot4(xb[t].w, 0x01010101u, cs);
             xsv[t] = LPG == 4 ? quad_sum(cs) : cs;
-            // workgroup 0 hands the quantised activations to later consumers
             if (blockIdx.x == 0 && slot == 0 && kact && t < a.M) {
-                int8_t* xo = p.qin.xq + tt * a.K + kpos;
-                *reinterpret_cast<uint4*>(xo) = xa[t];
-                *reinterpret_cast<uint4*>(xo + 16) = xb[t];
-                if ((lane % LPG) == 0) p.qin.xs[tt * NE + e] = xsv[t];
-                if (tid == 0) p.qin.dx[tt] = d;
+                if ((lane % LPG) == 0) p.qin.xs[(int64_t)t * NE + e] = xsv[t];
+                if (tid == 0) p.qin.dx[t] = dxv[t];
             }
         }
     }
@@ -456,7 +496,7 @@ Plan make_plan(const LinearArgs& a, bool argmax, bool qin = false) {
         size_t b = (size_t)p.MT * nh * rb * p.NEP * 4 + (size_t)nh * rb * p.NG * 8 +
                    (size_t)p.MT * p.NE * 4 + (size_t)p.MT * (pt ? 1 : a.K / 32) * 4;
         if (argmax) b += 16 + (size_t)p.MT * rb * 8;
-        if (qin) b += (size_t)p.MT * (8 + 16) * 4;
+        if (qin) b += (size_t)p.MT * (16 * 4 + 8 * 64 * 4 + a.K) + 16;
         return b;
     };
     // registers: weights in flight (4 per row half) + activations (8 per token)

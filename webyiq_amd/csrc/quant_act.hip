@@ -1,9 +1,25 @@
-// Lane l of wave w owns the 32-element slices 2048 j + 32 l of the passes
-// j = w, w + 4, ... of its token's row -- the slice a decode GEMV lane owns --
-// and every reduction that feeds a rounding (the RMSNorm sum of squares) runs
-// in a fixed order the CPU oracle restates: an fmaf chain per slice, a
-// wavefront xor butterfly per pass, pass sums added in pass order.  So int8
-// codes are reproducible bit for bit, here and in the fused GEMV quantiser.
+// Activation quantiser (webyIQ crates/engine/src/shaders/quant.wgsl:19-62 and
+// the torch fake-quant hook tools/reference.py:43-48).
+//
+//   optional RMSNorm: v = (x * r) * nw, r = 1 / sqrt(mean(x^2) + eps)
+//   per activation group (GA = K or 32): dx = amax / 127,
+//   xq = dx > 0 ? round_half_even(v / dx) : 0   (IEEE division, as torch)
+//   xs[e] = sum of xq over accumulation group e (Ge = min(G, GA) elements)
+//
+// The row is read in passes of 2048 elements (512 float4 chunks): load u
+// (0..7) of pass j gives lane l the chunk 512 j + 64 u + l, so every load
+// instruction reads 1 KiB of consecutive memory and every code store writes
+// 256 consecutive bytes.  The RMSNorm sum of squares, the one reduction that
+// feeds a rounding, runs in a fixed order the CPU oracle restates: an fmaf
+// chain per chunk, a pairwise tree over a lane's 8 chunks, a pairwise tree
+// over the 64 lanes (wave_sum_tree), pass sums added in pass order.  The tree
+// over a lane's chunks lets waves that hold 2, 4 or 8 of its loads form the
+// same value, so codes are bit-identical across the kernels below and the
+// fused GEMV quantiser.
+//
+// Two layouts: few tokens -- one workgroup per token, wave w taking loads 2w
+// and 2w + 1 of every pass (latency); many tokens -- one wavefront per token,
+// four tokens per workgroup, no barriers (throughput).
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -14,185 +30,256 @@ namespace {
 
 constexpr int kQuantThreads = 256;
 constexpr int kQuantWaves = kQuantThreads / 64;
-constexpr int kPass = 2048;  // codes per wavefront pass (64 lanes x 32)
+constexpr int kPassChunks = 512;   // float4 chunks per 2048-element pass
+constexpr int kSplitMaxPasses = 8; // split layout: K <= 16384
+constexpr int kSplitMaxTokens = 16;
 
-// CACHED (K <= 4 passes): one slice per lane, loaded once and kept in
-// registers.  Longer rows are re-read (L2 hits) in each phase.
-template <bool NORM, bool PER_TOKEN, int GE, bool CACHED>
-__global__ __launch_bounds__(kQuantThreads) void quant_act_kernel(QuantArgs a) {
+__device__ __forceinline__ float4 normed(float4 v, float r, float4 w) {
+    v.x = (v.x * r) * w.x;
+    v.y = (v.y * r) * w.y;
+    v.z = (v.z * r) * w.z;
+    v.w = (v.w * r) * w.w;
+    return v;
+}
+
+__device__ __forceinline__ float absmax4(float4 v) {
+    return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
+__device__ __forceinline__ uint32_t pack_codes(float4 v, float d, float rd, int& sum) {
+    int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+    if (d > 0.0f) {
+        q0 = quant_code(v.x, d, rd);
+        q1 = quant_code(v.y, d, rd);
+        q2 = quant_code(v.z, d, rd);
+        q3 = quant_code(v.w, d, rd);
+    }
+    sum = q0 + q1 + q2 + q3;
+    return (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+           ((uint32_t)(q3 & 0xFF) << 24);
+}
+
+// Codes, per-32 scales and group sums of one load (64 consecutive chunks
+// starting at chunk c - lane) of token t.
+template <bool PER_TOKEN, int GE>
+__device__ __forceinline__ void emit(const QuantArgs& a, int64_t t, int c, bool valid, float4 v, float dtok,
+                                     float rtok, int lane) {
+    float d = dtok, rd = rtok;
+    if (!PER_TOKEN) {
+        // the 32-element activation group = 8 consecutive lanes
+        d = max8(absmax4(v)) / 127.0f;
+        rd = 1.0f / d;
+        if (valid && (lane & 7) == 0) a.dx[t * (a.K / 32) + c / 8] = d;
+    }
+    int sum;
+    const uint32_t wd = pack_codes(valid ? v : make_float4(0.f, 0.f, 0.f, 0.f), d, rd, sum);
+    if (valid) reinterpret_cast<uint32_t*>(a.xq + t * a.K)[c] = wd;
+    if (GE == 32) {
+        const int s8 = sum8(sum);
+        if (valid && (lane & 7) == 0) a.xs[t * (a.K / 32) + c / 8] = s8;
+    } else {
+        const int s32 = sum32_rows13(sum);
+        if (valid && (lane & 31) == 16) a.xs[t * (a.K / 128) + c / 32] = s32;
+    }
+}
+
+// One workgroup per token; wave w holds loads 2w, 2w + 1 of every pass.
+template <bool NORM, bool PER_TOKEN, int GE>
+__global__ __launch_bounds__(kQuantThreads) void quant_split_kernel(QuantArgs a) {
     pin_arg(a.x); pin_arg(a.norm_w); pin_arg(a.eps); pin_arg(a.K);
     pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t t = blockIdx.x;
     const int K = (int)a.K;
-    const int J = (K + kPass - 1) / kPass;
-    const int NL = CACHED ? 1 : (J - wave + kQuantWaves - 1) / kQuantWaves;  // this wave's passes
-    const float* xr = a.x + t * a.K;
-    __shared__ float red[kQuantWaves];
+    const int nchunk = K / 4;
+    const int J = (nchunk + kPassChunks - 1) / kPassChunks;
+    const float4* xr = reinterpret_cast<const float4*>(a.x + t * a.K);
+    const float4* nw = reinterpret_cast<const float4*>(a.norm_w);
+    __shared__ float sub[kSplitMaxPasses][kQuantWaves][64];  // per-wave lane subtrees
+    __shared__ float red[kSplitMaxPasses];
+    __shared__ float wred[kQuantWaves];
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
 
-    // slice i of this lane: pass j = wave + 4 i, codes [base, base + 32)
-    auto base_of = [&](int i) { return kPass * (wave + kQuantWaves * i) + 32 * lane; };
-    auto load_slice = [&](int b, float4* v) {
-        const float4* p = reinterpret_cast<const float4*>(xr + b);
+    float4 xc[kSplitMaxPasses][2], wc[kSplitMaxPasses][2];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = p[u];
-    };
-    float4 xc[8], wc[8];
-    const bool act0 = base_of(0) < K && wave < J;
-    if (CACHED) {
-        load_slice(act0 ? base_of(0) : 0, xc);
-        if (NORM) {
-            const float4* p = reinterpret_cast<const float4*>(a.norm_w + (act0 ? base_of(0) : 0));
+    for (int j = 0; j < kSplitMaxPasses; ++j)
 #pragma unroll
-            for (int u = 0; u < 8; ++u) wc[u] = p[u];
+        for (int i = 0; i < 2; ++i) {
+            const int c = kPassChunks * j + 64 * (2 * wave + i) + lane;
+            const bool ok = j < J && c < nchunk;
+            xc[j][i] = ok ? xr[c] : zero4;
+            if (NORM) wc[j][i] = ok ? nw[c] : zero4;
         }
-    }
-    // this lane's slice i as (optionally normalised) values
+
     float r = 1.0f;
-    auto slice = [&](int i, float4* v) {
-        const int b = base_of(i);
-        if (CACHED) {
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = xc[u];
-        } else {
-            load_slice(b, v);
-        }
-        if (NORM) {
-            const float4* p = reinterpret_cast<const float4*>(a.norm_w + b);
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float4 w = CACHED ? wc[u] : p[u];
-                v[u].x = (v[u].x * r) * w.x;
-                v[u].y = (v[u].y * r) * w.y;
-                v[u].z = (v[u].z * r) * w.z;
-                v[u].w = (v[u].w * r) * w.w;
-            }
-        }
-    };
-
     if (NORM) {
-        // rounds of 4 passes: wave w adds pass 4 q + w; every thread then adds
-        // the round's pass sums in pass order
-        float total = 0.0f;
-        const int rounds = (J + kQuantWaves - 1) / kQuantWaves;
-        for (int q = 0; q < rounds; ++q) {
-            const int b = kPass * (wave + kQuantWaves * q) + 32 * lane;
-            float pp = 0.0f;
-            if (wave + kQuantWaves * q < J && b < K) {
-                float4 v[8];
-                if (CACHED) {
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) v[u] = xc[u];
-                } else {
-                    load_slice(b, v);
-                }
+        for (int j = 0; j < kSplitMaxPasses; ++j)
+            if (j < J) sub[j][wave][lane] = chunk_ss(xc[j][0]) + chunk_ss(xc[j][1]);
+        __syncthreads();
+        // wave w completes passes w, w + 4: the lane tree, then the lane tree
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    pp = fmaf(v[u].x, v[u].x, pp);
-                    pp = fmaf(v[u].y, v[u].y, pp);
-                    pp = fmaf(v[u].z, v[u].z, pp);
-                    pp = fmaf(v[u].w, v[u].w, pp);
-                }
+        for (int q = 0; q < kSplitMaxPasses / kQuantWaves; ++q) {
+            const int j = wave + kQuantWaves * q;
+            if (j < J) {
+                const float p = (sub[j][0][lane] + sub[j][1][lane]) + (sub[j][2][lane] + sub[j][3][lane]);
+                const float s = wave_sum_tree(p);
+                if (lane == 0) red[j] = s;
             }
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) pp = pp + __shfl_xor(pp, o);
-            if (lane == 0) red[wave] = pp;
-            __syncthreads();
-            const int np = min(kQuantWaves, J - kQuantWaves * q);
-            for (int w = 0; w < np; ++w) total = total + red[w];
-            __syncthreads();
         }
+        __syncthreads();
+        float total = 0.0f;
+        for (int j = 0; j < J; ++j) total = total + red[j];
         r = 1.0f / sqrt_rn(total / (float)K + a.eps);
     }
 
-    // Per-token scale: block-wide absolute maximum (exact, order-free).
     float dtok = 0.0f;
     if (PER_TOKEN) {
         float m = 0.0f;
-        for (int i = 0; i < NL; ++i) {
-            if (base_of(i) >= K || (CACHED && !act0)) continue;
-            float4 v[8];
-            slice(i, v);
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                m = fmaxf(m, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
-        }
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        if (lane == 0) red[wave] = m;
+        for (int j = 0; j < kSplitMaxPasses; ++j)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int c = kPassChunks * j + 64 * (2 * wave + i) + lane;
+                if (j < J && c < nchunk) m = fmaxf(m, absmax4(NORM ? normed(xc[j][i], r, wc[j][i]) : xc[j][i]));
+            }
+        m = wave_max(m);
+        if (lane == 0) wred[wave] = m;
         __syncthreads();
-        float amax = red[0];
-        for (int w = 1; w < kQuantWaves; ++w) amax = fmaxf(amax, red[w]);
+        const float amax = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
         dtok = amax / 127.0f;
         if (tid == 0) a.dx[t] = dtok;
     }
-
-    for (int i = 0; i < NL; ++i) {
-        const int b = base_of(i);
-        const bool valid = b < K && (!CACHED || act0);
-        float4 v[8];
-        if (valid) {
-            slice(i, v);
-        } else {
+    const float rtok = 1.0f / dtok;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        float d = dtok;
-        if (!PER_TOKEN) {
-            // the slice is one 32-element activation group
-            float m = 0.0f;
+    for (int j = 0; j < kSplitMaxPasses; ++j) {
+        if (j >= J) break;
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                m = fmaxf(m, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
-            d = m / 127.0f;
-            if (valid) a.dx[t * (a.K / 32) + b / 32] = d;
-        }
-        uint32_t wds[8];
-        int cs = 0;
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
-            if (d > 0.0f) {
-                q0 = (int)rintf(v[u].x / d);
-                q1 = (int)rintf(v[u].y / d);
-                q2 = (int)rintf(v[u].z / d);
-                q3 = (int)rintf(v[u].w / d);
-            }
-            wds[u] = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
-                     ((uint32_t)(q3 & 0xFF) << 24);
-            cs += q0 + q1 + q2 + q3;
-        }
-        if (GE == 128) cs = quad_sum(cs);  // 4 consecutive lanes = one 128-group
-        if (valid) {
-            uint4* xo = reinterpret_cast<uint4*>(a.xq + t * a.K + b);
-            xo[0] = make_uint4(wds[0], wds[1], wds[2], wds[3]);
-            xo[1] = make_uint4(wds[4], wds[5], wds[6], wds[7]);
-            if ((lane % (GE / 32)) == 0) a.xs[t * (a.K / GE) + b / GE] = cs;
+        for (int i = 0; i < 2; ++i) {
+            const int c = kPassChunks * j + 64 * (2 * wave + i) + lane;
+            const float4 v = NORM ? normed(xc[j][i], r, wc[j][i]) : xc[j][i];
+            emit<PER_TOKEN, GE>(a, t, c, c < nchunk, v, dtok, rtok, lane);
         }
     }
 }
 
-template <bool NORM, bool CACHED>
-hipError_t dispatch_quant(const QuantArgs& a, hipStream_t s) {
-    dim3 grid((unsigned)a.M), block(kQuantThreads);
-    bool pt = a.GA == a.K;
-    int ge = a.GA < a.G ? a.GA : a.G;
-    if (pt && ge == 128)
-        hipLaunchKernelGGL((quant_act_kernel<NORM, true, 128, CACHED>), grid, block, 0, s, a);
-    else if (pt && ge == 32)
-        hipLaunchKernelGGL((quant_act_kernel<NORM, true, 32, CACHED>), grid, block, 0, s, a);
+// One wavefront per token, 4 tokens per workgroup, no barriers.  JC > 0:
+// rows of at most JC passes stay in registers; JC == 0: longer rows are
+// re-read (L2 hits) in each phase.
+template <bool NORM, bool PER_TOKEN, int GE, int JC>
+__global__ __launch_bounds__(kQuantThreads) void quant_wave_kernel(QuantArgs a) {
+    pin_arg(a.x); pin_arg(a.norm_w); pin_arg(a.eps); pin_arg(a.K); pin_arg(a.M);
+    pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
+    const int lane = threadIdx.x & 63;
+    const int64_t t = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
+    if (t >= a.M) return;  // whole wavefronts; the kernel has no barrier
+    const int K = (int)a.K;
+    const int nchunk = K / 4;
+    const int J = (nchunk + kPassChunks - 1) / kPassChunks;
+    const float4* xr = reinterpret_cast<const float4*>(a.x + t * a.K);
+    const float4* nw = reinterpret_cast<const float4*>(a.norm_w);
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto chunk = [&](int j, int u) { return kPassChunks * j + 64 * u + lane; };
+
+    constexpr int NC = JC > 0 ? JC : 1;
+    float4 xc[NC][8], wc[NC][8];
+    if (JC > 0) {
+#pragma unroll
+        for (int j = 0; j < NC; ++j)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int c = chunk(j, u);
+                const bool ok = j < J && c < nchunk;
+                xc[j][u] = ok ? xr[c] : zero4;
+                if (NORM) wc[j][u] = ok ? nw[c] : zero4;
+            }
+    }
+    auto raw = [&](int j, int u) -> float4 {
+        if (JC > 0) return xc[JC > 0 ? j : 0][u];
+        const int c = chunk(j, u);
+        return c < nchunk ? xr[c] : zero4;
+    };
+    auto nwt = [&](int j, int u) -> float4 {
+        if (JC > 0) return wc[JC > 0 ? j : 0][u];
+        const int c = chunk(j, u);
+        return c < nchunk ? nw[c] : zero4;
+    };
+    // f(j) for every pass; constant j (registers) when the row is cached
+    auto for_passes = [&](auto&& f) {
+        if constexpr (JC > 0) {
+#pragma unroll
+            for (int j = 0; j < NC; ++j)
+                if (j < J) f(j);
+        } else {
+            for (int j = 0; j < J; ++j) f(j);
+        }
+    };
+
+    float r = 1.0f;
+    if (NORM) {
+        float total = 0.0f;
+        for_passes([&](int j) {
+            float c[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) c[u] = chunk_ss(raw(j, u));
+            const float p = ((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]));
+            total = total + wave_sum_tree(p);
+        });
+        r = 1.0f / sqrt_rn(total / (float)K + a.eps);
+    }
+    auto load = [&](int j, int u) -> float4 { return NORM ? normed(raw(j, u), r, nwt(j, u)) : raw(j, u); };
+
+    float dtok = 0.0f;
+    if (PER_TOKEN) {
+        float m = 0.0f;
+        for_passes([&](int j) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (chunk(j, u) < nchunk) m = fmaxf(m, absmax4(load(j, u)));
+        });
+        dtok = wave_max(m) / 127.0f;
+        if (lane == 0) a.dx[t] = dtok;
+    }
+    const float rtok = 1.0f / dtok;
+    for_passes([&](int j) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = chunk(j, u);
+            emit<PER_TOKEN, GE>(a, t, c, c < nchunk, load(j, u), dtok, rtok, lane);
+        }
+    });
+}
+
+template <bool NORM, bool PT, int GE>
+hipError_t dispatch_rows(const QuantArgs& a, hipStream_t s) {
+    const int64_t passes = (a.K + 4 * kPassChunks - 1) / (4 * kPassChunks);
+    if (a.M <= kSplitMaxTokens && passes <= kSplitMaxPasses) {
+        hipLaunchKernelGGL((quant_split_kernel<NORM, PT, GE>), dim3((unsigned)a.M), dim3(kQuantThreads), 0, s, a);
+        return hipGetLastError();
+    }
+    dim3 grid((unsigned)((a.M + kQuantWaves - 1) / kQuantWaves)), block(kQuantThreads);
+    if (passes <= 1)
+        hipLaunchKernelGGL((quant_wave_kernel<NORM, PT, GE, 1>), grid, block, 0, s, a);
+    else if (passes <= 3)
+        hipLaunchKernelGGL((quant_wave_kernel<NORM, PT, GE, 3>), grid, block, 0, s, a);
     else
-        hipLaunchKernelGGL((quant_act_kernel<NORM, false, 32, CACHED>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((quant_wave_kernel<NORM, PT, GE, 0>), grid, block, 0, s, a);
     return hipGetLastError();
+}
+
+template <bool NORM>
+hipError_t dispatch_format(const QuantArgs& a, hipStream_t s) {
+    const bool pt = a.GA == a.K;
+    const int ge = a.GA < a.G ? a.GA : a.G;
+    if (pt && ge == 128) return dispatch_rows<NORM, true, 128>(a, s);
+    if (pt && ge == 32) return dispatch_rows<NORM, true, 32>(a, s);
+    return dispatch_rows<NORM, false, 32>(a, s);
 }
 
 }  // namespace
 
 hipError_t launch_quant_act(const QuantArgs& a, hipStream_t s) {
-    const bool cached = a.K <= kQuantWaves * kPass;
-    if (a.norm_w) return cached ? dispatch_quant<true, true>(a, s) : dispatch_quant<true, false>(a, s);
-    return cached ? dispatch_quant<false, true>(a, s) : dispatch_quant<false, false>(a, s);
+    return a.norm_w ? dispatch_format<true>(a, s) : dispatch_format<false>(a, s);
 }
 
 }  // namespace wq
