@@ -72,6 +72,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     const int K = (int)a.K;
     const int RB = p.RB;
     const int NE = p.NE, NEP = p.NEP, NG = p.NG;
+    const int NGS = NG + 2;  // LDS row stride of the (s, m) pairs: rows on distinct banks
     const int NDX = PT ? 1 : K / 32;
     const int64_t r0 = (int64_t)blockIdx.x * RB;
 
@@ -79,7 +80,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     //      activation sums [MT][NE] f32 | activation scales [MT][NDX] f32
     int32_t* acc_lds = reinterpret_cast<int32_t*>(smem);
     float2* sm_lds = reinterpret_cast<float2*>(acc_lds + (size_t)MT * NH * RB * NEP);
-    float* xs_lds = reinterpret_cast<float*>(sm_lds + (size_t)NH * RB * NG);
+    float* xs_lds = reinterpret_cast<float*>(sm_lds + (size_t)NH * RB * NGS);
     float* dx_lds = xs_lds + (size_t)MT * NE;
     // fused quantiser scratch (QIN kernels have no argmax keys)
     static_assert(!(QIN && ARGMAX), "no fused quantiser in the lm_head kernel");
@@ -125,6 +126,24 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         asm volatile("" ::: "memory");
     }
 
+    uint4 xa[MT], xb[MT];
+    int32_t xsv[MT];
+    float dxv[MT];
+    if constexpr (!QIN) {
+        // the activations first (a few KiB, L2-resident): row s's products
+        // can then start as soon as its weights land
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            int64_t tt = t < a.M ? t : a.M - 1;
+            const unsigned char* xp = reinterpret_cast<const unsigned char*>(a.xq) + tt * a.K + kpos;
+            xa[t] = load16(xp);
+            xb[t] = load16(xp + 16);
+            xsv[t] = a.xs[tt * NE + e];
+            dxv[t] = a.dx[tt * NDX + (PT ? 0 : e)];
+        }
+        asm volatile("" ::: "memory");  // keep them ahead of the weight stream
+    }
+
     // 1. issue every global load of this lane before the first one is consumed
     //    (one memory round trip; rows past N re-read row N-1)
     uint4 wv[NH][IPW];
@@ -138,21 +157,9 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
             wv[h][s] = load_stream16(wbase + (size_t)(row + h * N) * row_bytes);
             sv[h][s] = a.ws[(row + h * N) * NG + g];
         }
+        asm volatile("" ::: "memory");  // loads stay in row order: row s lands before row s + 1
     }
-    uint4 xa[MT], xb[MT];
-    int32_t xsv[MT];
-    float dxv[MT];
-    if constexpr (!QIN) {
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            int64_t tt = t < a.M ? t : a.M - 1;
-            const unsigned char* xp = reinterpret_cast<const unsigned char*>(a.xq) + tt * a.K + kpos;
-            xa[t] = load16(xp);
-            xb[t] = load16(xp + 16);
-            xsv[t] = a.xs[tt * NE + e];
-            dxv[t] = a.dx[tt * NDX + (PT ? 0 : e)];
-        }
-    } else {
+    if constexpr (QIN) {
         // Fused per-token quantiser, while the weight loads are in flight:
         // the quant_act kernels' arithmetic and reduction order (per-chunk
         // fmaf chains, a pairwise tree over a lane's 8 chunks -- here split
@@ -275,83 +282,55 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         }
     }
 
-    // 2. activation sums / scales and weight (s, m) -> LDS
-    if (slot == 0 && kact && (lane % LPG) == 0) {
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            xs_lds[t * NE + e] = (float)xsv[t];
-            if (!PT) dx_lds[t * NDX + e] = dxv[t];
-        }
-    }
-    if (PT && tid == 0) {
-#pragma unroll
-        for (int t = 0; t < MT; ++t) dx_lds[t] = dxv[t];
-    }
-    if (kact && (lane % LPW) == 0) {
-#pragma unroll
-        for (int s = 0; s < IPW; ++s)
-#pragma unroll
-            for (int h = 0; h < NH; ++h)
-                sm_lds[(h * RB + slot + p.nslots * s) * NG + g] = make_float2(f16lo(sv[h][s]), f16hi(sv[h][s]));
-    }
-
-    // 3. exact int32 group sums -> LDS
-#pragma unroll
-    for (int s = 0; s < IPW; ++s) {
-        const int rl = slot + p.nslots * s;
-#pragma unroll
-        for (int h = 0; h < NH; ++h) {
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                int d = dot32(wv[h][s], xa[t], xb[t]);
-                if (LPG == 4) d = quad_sum(d);
-                if (kact && (lane % LPG) == 0) acc_lds[((t * NH + h) * RB + rl) * NEP + e] = d;
-            }
-        }
-    }
-    __syncthreads();
-
-    if (a.acc_dump) {  // test hook: the group sums exactly as the epilogue reads them
-        const int rows_total = NH * (int)N;
-        for (int i = tid; i < MT * NH * RB * NE; i += nthreads) {
-            int ee = i % NE;
-            int rl = (i / NE) % RB;
-            int h = (i / (NE * RB)) % NH;
-            int t = i / (NE * RB * NH);
-            int64_t row = r0 + rl;
-            if (t < a.M && row < N)
-                a.acc_dump[((int64_t)t * rows_total + h * N + row) * NE + ee] =
-                    acc_lds[((t * NH + h) * RB + rl) * NEP + ee];
-        }
-    }
-
-    // 4. fp32 epilogue: one chain per (token, row) over the groups in order
+    // fp32 epilogue: one chain per (token, row) over the groups in order
     auto chain = [&](int t, int h, int rl) -> float {
         const int32_t* ar = acc_lds + ((t * NH + h) * RB + rl) * NEP;
-        const float2* sr = sm_lds + (h * RB + rl) * NG;
+        const float2* sr = sm_lds + (h * RB + rl) * NGS;
         const float* xsr = xs_lds + t * NE;
         const float* dr = dx_lds + t * NDX;
         float acc = 0.0f;
         if (PT) {
             int ee = 0;
+            // the (A, X, s, m) operands of a block are read before its fma
+            // chain: one LDS round trip per 16 groups (same fma order)
+            auto block4 = [&](int e0, float& acc_) {
+                const int4 a4 = *reinterpret_cast<const int4*>(ar + e0);
+                const float4 x4 = *reinterpret_cast<const float4*>(xsr + e0);
+                const float4 w01 = *reinterpret_cast<const float4*>(sr + e0);
+                const float4 w23 = *reinterpret_cast<const float4*>(sr + e0 + 2);
+                acc_ = fmaf(w01.x, (float)a4.x, acc_);
+                acc_ = fmaf(w01.y, x4.x, acc_);
+                acc_ = fmaf(w01.z, (float)a4.y, acc_);
+                acc_ = fmaf(w01.w, x4.y, acc_);
+                acc_ = fmaf(w23.x, (float)a4.z, acc_);
+                acc_ = fmaf(w23.y, x4.z, acc_);
+                acc_ = fmaf(w23.z, (float)a4.w, acc_);
+                acc_ = fmaf(w23.w, x4.w, acc_);
+            };
             if ((NE & 3) == 0) {
-                // 16-byte LDS reads, 4 groups per block, all of a block's
-                // operands read before its fma chain (same fma order)
-#pragma unroll 4
-                for (; ee < NE; ee += 4) {
-                    const int4 a4 = *reinterpret_cast<const int4*>(ar + ee);
-                    const float4 x4 = *reinterpret_cast<const float4*>(xsr + ee);
-                    const float4 w01 = *reinterpret_cast<const float4*>(sr + ee);
-                    const float4 w23 = *reinterpret_cast<const float4*>(sr + ee + 2);
-                    acc = fmaf(w01.x, (float)a4.x, acc);
-                    acc = fmaf(w01.y, x4.x, acc);
-                    acc = fmaf(w01.z, (float)a4.y, acc);
-                    acc = fmaf(w01.w, x4.y, acc);
-                    acc = fmaf(w23.x, (float)a4.z, acc);
-                    acc = fmaf(w23.y, x4.z, acc);
-                    acc = fmaf(w23.z, (float)a4.w, acc);
-                    acc = fmaf(w23.w, x4.w, acc);
+                for (; ee + 16 <= NE; ee += 16) {
+                    int4 a4[4];
+                    float4 x4[4], w01[4], w23[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        a4[q] = *reinterpret_cast<const int4*>(ar + ee + 4 * q);
+                        x4[q] = *reinterpret_cast<const float4*>(xsr + ee + 4 * q);
+                        w01[q] = *reinterpret_cast<const float4*>(sr + ee + 4 * q);
+                        w23[q] = *reinterpret_cast<const float4*>(sr + ee + 4 * q + 2);
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        acc = fmaf(w01[q].x, (float)a4[q].x, acc);
+                        acc = fmaf(w01[q].y, x4[q].x, acc);
+                        acc = fmaf(w01[q].z, (float)a4[q].y, acc);
+                        acc = fmaf(w01[q].w, x4[q].y, acc);
+                        acc = fmaf(w23[q].x, (float)a4[q].z, acc);
+                        acc = fmaf(w23[q].y, x4[q].z, acc);
+                        acc = fmaf(w23[q].z, (float)a4[q].w, acc);
+                        acc = fmaf(w23[q].w, x4[q].w, acc);
+                    }
                 }
+                for (; ee < NE; ee += 4) block4(ee, acc);
             }
 #pragma unroll 8
             for (; ee < NE; ++ee) {
@@ -371,20 +350,68 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
             return acc;
         }
     };
+    // y of (token t, local row rl) from its chain(s)
+    auto finish = [&](int t, int rl) {
+        const float v = chain(t, 0, rl);
+        float* yo = a.y + (int64_t)t * N + r0 + rl;
+        if (MODE == 0) {
+            *yo = v;
+        } else if (MODE == 1) {
+            *yo = *yo + v;
+        } else {
+            *yo = silu_mul(v, chain(t, 1, rl));
+        }
+    };
+    // 2. activation sums / scales and weight (s, m) -> LDS
+    if (slot == 0 && kact && (lane % LPG) == 0) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            xs_lds[t * NE + e] = (float)xsv[t];
+            if (!PT) dx_lds[t * NDX + e] = dxv[t];
+        }
+    }
+    if (PT && tid == 0) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) dx_lds[t] = dxv[t];
+    }
+
+    // 3. per row, in load order (each row as soon as its loads land): the
+    //    weight (s, m) pairs and the exact int32 group sums -> LDS
+#pragma unroll
+    for (int s = 0; s < IPW; ++s) {
+        const int rl = slot + p.nslots * s;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                int d = dot32(wv[h][s], xa[t], xb[t]);
+                if (LPG == 4) d = quad_sum(d);
+                if (kact && (lane % LPG) == 0) acc_lds[((t * NH + h) * RB + rl) * NEP + e] = d;
+            }
+            if (kact && (lane % LPW) == 0)
+                sm_lds[(h * RB + rl) * NGS + g] = make_float2(f16lo(sv[h][s]), f16hi(sv[h][s]));
+        }
+    }
+    __syncthreads();
+
+    if (a.acc_dump) {  // test hook: the group sums exactly as the epilogue reads them
+        const int rows_total = NH * (int)N;
+        for (int i = tid; i < MT * NH * RB * NE; i += nthreads) {
+            int ee = i % NE;
+            int rl = (i / NE) % RB;
+            int h = (i / (NE * RB)) % NH;
+            int t = i / (NE * RB * NH);
+            int64_t row = r0 + rl;
+            if (t < a.M && row < N)
+                a.acc_dump[((int64_t)t * rows_total + h * N + row) * NE + ee] =
+                    acc_lds[((t * NH + h) * RB + rl) * NEP + ee];
+        }
+    }
+
     if (!ARGMAX) {
         for (int o = tid; o < MT * RB; o += nthreads) {
-            const int t = o / RB, rl = o - t * RB;
-            const int64_t row = r0 + rl;
-            if (t >= a.M || row >= N) continue;
-            float v = chain(t, 0, rl);
-            float* yo = a.y + (int64_t)t * N + row;
-            if (MODE == 0) {
-                *yo = v;
-            } else if (MODE == 1) {
-                *yo = *yo + v;
-            } else {
-                *yo = silu_mul(v, chain(t, 1, rl));
-            }
+            const int t = MT == 1 ? 0 : o / RB, rl = o - t * RB;
+            if (t < a.M && r0 + rl < N) finish(t, rl);
         }
         return;
     }
@@ -486,14 +513,17 @@ Plan make_plan(const LinearArgs& a, bool argmax, bool qin = false) {
     // kGemvTargetWgs workgroups (every CU busy, all loads issued up front)
     int ipw = 8;
     static const int choices[] = {1, 2, 4, 6, 8};
+    // (gate + up pairs and 8-token launches carry twice the epilogue work per
+    // row: 1.5x the workgroups measured faster for them)
+    const int64_t target = (a.mode == 2 || p.MT == 8) ? kGemvTargetWgs * 3 / 2 : kGemvTargetWgs;
     for (int c : choices) {
         int64_t rb = (int64_t)p.nslots * c;
-        if ((a.N + rb - 1) / rb <= kGemvTargetWgs) { ipw = c; break; }
+        if ((a.N + rb - 1) / rb <= target) { ipw = c; break; }
     }
     // LDS budget: 64 KiB per workgroup
     auto lds_of = [&](int ipw_) {
         size_t rb = (size_t)p.nslots * ipw_;
-        size_t b = (size_t)p.MT * nh * rb * p.NEP * 4 + (size_t)nh * rb * p.NG * 8 +
+        size_t b = (size_t)p.MT * nh * rb * p.NEP * 4 + (size_t)nh * rb * (p.NG + 2) * 8 +
                    (size_t)p.MT * p.NE * 4 + (size_t)p.MT * (pt ? 1 : a.K / 32) * 4;
         if (argmax) b += 16 + (size_t)p.MT * rb * 8;
         if (qin) b += (size_t)p.MT * (16 * 4 + 8 * 64 * 4 + a.K) + 16;
