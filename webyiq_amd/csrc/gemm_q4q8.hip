@@ -42,6 +42,7 @@ constexpr int kXcds = 8;          // MI355X: 8 XCDs, workgroups dispatched round
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 struct GemmParams {
@@ -137,8 +138,13 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     constexpr int X_SZ = FAST ? 16 : NES * BM * 4, D_SZ = PT ? 16 : NES * BM * 4;
     constexpr int ST_SZ = A_SZ + B_SZ + S_SZ + X_SZ + D_SZ;
     constexpr int RED_SZ = KS > 1 ? kWaveGroup * TM * TN * 16 * 4 : 0;
-    constexpr int LDS_SZ = NST * ST_SZ > RED_SZ ? NST * ST_SZ : RED_SZ;
+    constexpr int NWAVES = gemm_threads(G, PT) / 64;
+    constexpr int TR_STRIDE = 36;  // floats per row of a wave's 32 x 32 output transpose (16-byte rows)
+    constexpr int TR_SZ = NWAVES * 32 * TR_STRIDE * 4;
+    constexpr int BODY_SZ = NST * ST_SZ > RED_SZ ? NST * ST_SZ : RED_SZ;
+    constexpr int LDS_SZ = (BODY_SZ > TR_SZ ? BODY_SZ : TR_SZ) + BM * 4;  // + the tile's per-token scales
     __shared__ __align__(1024) unsigned char lds[LDS_SZ];
+    float* dx_tile = reinterpret_cast<float*>(lds + LDS_SZ - BM * 4);
     auto As = [&](int st) -> int8_t* { return reinterpret_cast<int8_t*>(lds + st * ST_SZ); };
     auto Bs = [&](int st) -> uint32_t* { return reinterpret_cast<uint32_t*>(lds + st * ST_SZ + A_SZ); };
     auto Ss = [&](int st) -> uint32_t* { return reinterpret_cast<uint32_t*>(lds + st * ST_SZ + A_SZ + B_SZ); };
@@ -247,6 +253,11 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
             for (int i = 0; i < D_PW; ++i) dma4(dxp, 4 * d_off[i], Ds(st) + 64 * (D_PW * wave + i));
         }
     };
+
+    // the tile's per-token scales for the epilogue, ahead of the ring loads
+    // (every wait below also covers them)
+    if (PT && wave < BM / 64 && (KS == 1 || wk == 0))
+        dma4(a.dx, 4 * (uint32_t)trow(64 * wave + lane), dx_tile + 64 * wave);
 
     // prologue loads: one group loads steps 0 .. NST-2; two groups load
     // their first step each
@@ -504,52 +515,68 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
         ihi = wk + 1;
     }
 
-    // epilogue: per-token scale, output mode, store (mode 1 reads every old
-    // value of its outputs in one batch first)
+    // epilogue: per-token scale and output mode in registers, then each
+    // 32 x 32 subtile goes through a per-wave LDS transpose so that every lane
+    // stores 16 consecutive bytes of a row (8 lanes cover a 128-byte row
+    // segment) instead of single words down a column
+    __syncthreads();  // the ring and the exchange area are free again
     constexpr int JO = MODE == 2 ? TN / 2 : TN;
-    float dtok[TM][16];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-            dtok[i][r] = PT && i >= ilo && i < ihi ? a.dx[trow(arow(i, r))] : 1.0f;
-    float yold[MODE == 1 ? TM : 1][MODE == 1 ? JO : 1][16];
-    if (MODE == 1) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            if (i < ilo || i >= ihi) continue;
-#pragma unroll
-            for (int j = 0; j < JO; ++j) {
-                int64_t n = n0 + bcol(j);
-                n = n < N ? n : N - 1;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) yold[i][j][r] = a.y[trow(arow(i, r)) * N + n];
-            }
-        }
-    }
+    float* tr = reinterpret_cast<float*>(lds) + (tid >> 6) * (32 * TR_STRIDE);
+    const bool vec_ok = (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 && (N & 3) == 0;  // 16-byte rows chunks
+    float dtok[16];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         if (i < ilo || i >= ihi) continue;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t t = m0 + arow(i, r);
-            if (t >= M) continue;
-            const float d = dtok[i][r];
+        for (int r = 0; r < 16; ++r) dtok[r] = PT ? dx_tile[arow(i, r)] : 1.0f;
 #pragma unroll
-            for (int j = 0; j < JO; ++j) {
-                const int64_t n = n0 + bcol(j);
-                if (n >= N) continue;
-                const float v = PT ? facc[i][j][r] * d : facc[i][j][r];
-                float* yo = a.y + t * N + n;
-                if (MODE == 0) {
-                    *yo = v;
-                } else if (MODE == 1) {
-                    *yo = yold[i][j][r] + v;
-                } else {
-                    const float u = PT ? facc[i][j + TN / 2][r] * d : facc[i][j + TN / 2][r];
-                    *yo = silu_mul(v, u);
+        for (int j = 0; j < JO; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float v = PT ? facc[i][j][r] * dtok[r] : facc[i][j][r];
+                if (MODE == 2) v = silu_mul(v, PT ? facc[i][j + TN / 2][r] * dtok[r] : facc[i][j + TN / 2][r]);
+                tr[(8 * (r >> 2) + 4 * h + (r & 3)) * TR_STRIDE + l32] = v;
+            }
+            __builtin_amdgcn_wave_barrier();  // LDS operations of a wave complete in order
+            const int64_t c0 = n0 + bcol(j) - l32 + 4 * (lane & 7);  // first output column of this lane
+            float4 o[4], yo4[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int row = 8 * q + (lane >> 3);
+                o[q] = *reinterpret_cast<const float4*>(tr + row * TR_STRIDE + 4 * (lane & 7));
+            }
+            if (MODE == 1) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int64_t t = m0 + wm * 64 + 32 * i + 8 * q + (lane >> 3);
+                    yo4[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (t < M && vec_ok && c0 + 3 < N) yo4[q] = *reinterpret_cast<const float4*>(a.y + t * N + c0);
                 }
             }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t t = m0 + wm * 64 + 32 * i + 8 * q + (lane >> 3);
+                if (t >= M) continue;
+                float* yp = a.y + t * N + c0;
+                if (vec_ok && c0 + 3 < N) {
+                    float4 v = o[q];
+                    if (MODE == 1) {
+                        v.x = yo4[q].x + v.x;
+                        v.y = yo4[q].y + v.y;
+                        v.z = yo4[q].z + v.z;
+                        v.w = yo4[q].w + v.w;
+                    }
+                    // streamed: the output is not re-read here, and lines left
+                    // dirty in L2 would be written back at the end of the kernel
+                    __builtin_nontemporal_store(v4f{v.x, v.y, v.z, v.w}, reinterpret_cast<v4f*>(yp));
+                } else {
+                    const float vv[4] = {o[q].x, o[q].y, o[q].z, o[q].w};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (c0 + u < N) yp[u] = MODE == 1 ? yp[u] + vv[u] : vv[u];
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
         }
     }
 }
