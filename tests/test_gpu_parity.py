@@ -146,6 +146,12 @@ GEMV_CASES = [
     (2, 2048, 256, 32, 32, 1),       # reference-native: G = 32, GA = 32
     (3, 4096, 130, 128, 32, 2),
     (7, 3072, 96, 32, None, 0),      # K not a multiple of 2048
+    # 3..8 tokens, N >= 16384: the int8-MFMA GEMV (row blocks of 16, K split
+    # between waves when K > 2048)
+    (8, 2048, 16400, 128, None, 0),  # ragged last block
+    (5, 6144, 16384, 128, None, 1),  # K split in 4
+    (3, 2048, 20000, 128, None, 2),  # gate/up pairs
+    (4, 4096, 16384, 128, None, 0),  # K split in 2
 ]
 
 
@@ -290,7 +296,8 @@ def test_argmax_standalone():
 
 
 @pytest.mark.parametrize("M,V,G,mapped", [(1, 32768, 128, False), (8, 32768, 128, True),
-                                          (3, 5000, 32, False), (1, 151936, 128, False)])
+                                          (3, 5000, 32, False), (1, 151936, 128, False),
+                                          (5, 20000, 128, False), (8, 151936, 128, False)])
 def test_lm_head_argmax(M, V, G, mapped):
     note(f"lm_head M={M} V={V} G={G} mapped={mapped}")
     K = 2048

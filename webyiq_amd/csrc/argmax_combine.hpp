@@ -1,0 +1,66 @@
+// Cross-workgroup greedy argmax combine of the fused lm_head kernels
+// (argmax.wgsl:19-43 semantics: the maximum key wins; a key holds the
+// order-preserving value bits above the complemented index, so ties go to
+// the lowest index; 0 means no value qualified).
+#pragma once
+
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace wq {
+
+// Every workgroup calls this once with its best key for token tid in
+// threads tid < M (0 elsewhere).  No memory fence is used (a device-scope
+// release would write back the XCD's L2): keys and tickets live in
+// kArgmaxSlots cache lines; a workgroup's atomicMax returns before its
+// ticket is taken, and both are device-coherent atomics, so a ticket implies
+// the max landed.  The last workgroup of each slot takes a top ticket; the
+// last of those reduces the slots, writes the token (mapped through ids when
+// set) and clears the workspace for the next call.
+template <int MT>
+__device__ __forceinline__ void argmax_combine(const ArgmaxArgs& am, int M, int nblocks, unsigned long long best) {
+    __shared__ unsigned int last_block;
+    __shared__ unsigned long long slot_keys[kArgmaxSlots * MT];
+    const int tid = threadIdx.x, nthreads = blockDim.x;
+    const int kslot = (int)(blockIdx.x % kArgmaxSlots);
+    if (tid < MT && tid < M) {
+        const unsigned long long old = atomicMax(am.keys + kslot * kArgmaxSlotWords + tid, best);
+        asm volatile("" ::"v"(old));  // the returned value: this atomic has been performed
+    }
+    __syncthreads();
+    const int used = nblocks < kArgmaxSlots ? nblocks : kArgmaxSlots;
+    if (tid == 0) {
+        const unsigned in_slot = (unsigned)((nblocks - kslot + kArgmaxSlots - 1) / kArgmaxSlots);
+        unsigned int done = atomicAdd(am.ticket + kslot * kArgmaxSlotWords * 2, 1u);
+        bool last = false;
+        if (done == in_slot - 1) {
+            unsigned int top = atomicAdd(am.ticket + kArgmaxSlots * kArgmaxSlotWords * 2, 1u);
+            last = top == (unsigned)used - 1;
+        }
+        last_block = last;
+    }
+    __syncthreads();
+    if (last_block) {
+        // every slot key read at once (independent device-coherent loads),
+        // then reduced in LDS
+        for (int o = tid; o < used * MT; o += nthreads)
+            slot_keys[o] = __hip_atomic_load(am.keys + (o / MT) * kArgmaxSlotWords + (o % MT), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (tid < M) {
+            unsigned long long k = 0;
+            for (int sl = 0; sl < used; ++sl) k = slot_keys[sl * MT + tid] > k ? slot_keys[sl * MT + tid] : k;
+            uint32_t idx = k ? 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull) : 0u;
+            am.tok_out[tid] = am.ids ? am.ids[idx] : idx;
+        }
+        __syncthreads();
+        for (int o = tid; o < used * MT; o += nthreads)
+            __hip_atomic_store(am.keys + (o / MT) * kArgmaxSlotWords + (o % MT), 0ull, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        for (int o = tid; o <= used; o += nthreads)
+            __hip_atomic_store(am.ticket + (o < used ? o * kArgmaxSlotWords * 2 : kArgmaxSlots * kArgmaxSlotWords * 2),
+                               0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+}  // namespace wq

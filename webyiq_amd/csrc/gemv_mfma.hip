@@ -1,0 +1,310 @@
+// Decode GEMV for 3..8 tokens and long outputs (N >= 16384: the lm_head) on
+// int8 MFMA, per-token activations and weight group 128 (the BASELINE format) -- the operator of gemv_q4q8.hip (webyIQ
+// crates/engine/src/shaders/gemv_q4q8.wgsl:36-131, Builder::gemv
+// graph.rs:190-198; the lm_head + greedy argmax of graph.rs:476-486 with
+// ARGMAX), for the token counts where the dot4 kernel's per-token VALU work
+// (8 dot4 + a DPP quad sum + an LDS write per token, row and lane) bounds it.
+//
+// A workgroup of 4 waves owns RB = 16 * RBW weight rows: RBW blocks of 16
+// rows, each block's K split between 4 / RBW waves (at most 16 groups per
+// wave).  Per 128-group a wave runs two v_mfma_i32_16x16x64_i8, tokens x
+// rows: lane l supplies token l % 16 of the activations and row l % 16 of
+// the weights, both for codes 32 q .. 32 q + 31 of the group (q = l / 16;
+// 16 codes per MFMA), the same code subset for both operands, so each
+// result is an exact int32 group sum.  Weight chunks (16 bytes per lane and
+// group) are all issued before the first is used; the int8 activations are
+// staged in LDS once per workgroup.  The group sums go to LDS and the fp32
+// epilogue is the dot4 kernel's -- one chain per (token, row) over the groups
+// in index order, acc = fma(s, A, acc); acc = fma(m, X, acc); y = acc * dx
+// -- so outputs are bit-identical to it and to the oracle.
+#include "argmax_combine.hpp"
+#include "common.hpp"
+#include "launch.hpp"
+
+#pragma clang fp contract(off)
+
+namespace wq {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kMaxGpw = 16;  // groups per wave
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Direct global -> LDS loads of 16 (4) bytes per lane: lane l's bytes land at
+// LDS address lds + 16 l (4 l); base and lds are wave-uniform.  Inline
+// assembly, so that the compiler's wait-count pass leaves them to the
+// explicit wait below.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)p);
+}
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, const void* lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 ::"v"(off), "s"(uniform_ptr(base)), "s"(lds_addr(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, const void* lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+                 ::"v"(off), "s"(uniform_ptr(base)), "s"(lds_addr(lds)) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+struct MfmaGemvParams {
+    LinearArgs a;
+    ArgmaxArgs am;
+    int NG;       // groups per row = K / 128
+    int NGP;      // LDS row stride of the group sums / scale pairs (16-byte rows)
+    int gpw;      // groups per wave = ceil(NG / KSPLIT)
+    int nblocks;  // gridDim.x
+};
+
+template <int MT, int MODE, int RBW, bool ARGMAX>
+__global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
+    constexpr int NH = MODE == 2 ? 2 : 1;  // gate (+ up) row halves
+    constexpr int RB = 16 * RBW;           // rows per workgroup
+    extern __shared__ __align__(16) unsigned char smem[];
+    const LinearArgs& a = p.a;
+    pin_arg(a.wq); pin_arg(a.ws); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs); pin_arg(a.y);
+    pin_arg(a.acc_dump); pin_arg(a.N); pin_arg(a.K); pin_arg(a.M);
+    pin_arg(p.NG); pin_arg(p.NGP); pin_arg(p.gpw);
+    if (ARGMAX) {
+        pin_arg(p.am.ids); pin_arg(p.am.tok_out); pin_arg(p.am.keys); pin_arg(p.am.ticket);
+        pin_arg(p.nblocks);
+    }
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int K = (int)a.K;
+    const int NG = p.NG, NGP = p.NGP, gpw = p.gpw;
+    const int64_t N = a.N;
+    const int blk = wave % RBW;       // this wave's row block
+    const int g0 = (wave / RBW) * gpw;  // its first group
+    const int ng = NG - g0 < gpw ? NG - g0 : gpw;  // its groups (>= 1: see the launcher)
+    const int64_t r0 = (int64_t)blockIdx.x * RB;
+    const int c = lane & 15, q = lane >> 4;
+
+    // LDS: group sums [MT][NH][RB][NGP] i32 | (s, m) [NH][RB][NGP] f32x2 |
+    //      activation group sums [MT * NG, 64-rounded] i32 | scales [64] f32 |
+    //      int8 activations [MT][K]
+    int32_t* acc_lds = reinterpret_cast<int32_t*>(smem);
+    float2* sm_lds = reinterpret_cast<float2*>(acc_lds + (size_t)MT * NH * RB * NGP);
+    int32_t* xs_lds = reinterpret_cast<int32_t*>(sm_lds + (size_t)NH * RB * NGP);
+    float* dx_lds = reinterpret_cast<float*>(xs_lds + ((MT * NG + 63) & ~63));
+    unsigned char* xq_lds = reinterpret_cast<unsigned char*>(dx_lds + 64);
+
+    // 1. the activations, their group sums and scales go global -> LDS
+    //    directly (no registers), issued first; then every weight chunk and
+    //    scale word of this lane, a fixed number of loads (groups past this
+    //    wave's last re-read it) so that one wait below covers exactly the
+    //    direct-to-LDS loads
+    const int xchunks = (int)(a.M * K / 16);  // 16-byte chunks of the real tokens
+    for (int base = 64 * wave; base < xchunks; base += 256)
+        dma16(a.xq, 16u * (uint32_t)(base + lane < xchunks ? base + lane : 0), xq_lds + 16 * base);
+    const int nxs = (int)a.M * NG;
+    for (int base = 64 * wave; base < nxs; base += 256)
+        dma4(a.xs, 4u * (uint32_t)(base + lane < nxs ? base + lane : 0), xs_lds + base);
+    if (wave == 0) dma4(a.dx, 4u * (uint32_t)(lane < a.M ? lane : 0), dx_lds);
+    int64_t row = r0 + 16 * blk + c;
+    row = row < N ? row : N - 1;
+    uint4 wv[NH][kMaxGpw];
+    uint32_t sv[NH][kMaxGpw / 4];
+#pragma unroll
+    for (int i = 0; i < kMaxGpw; ++i) {
+        const int gi = g0 + (i < ng ? i : ng - 1);
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+            wv[h][i] = load_stream16(reinterpret_cast<const unsigned char*>(a.wq) + (row + h * N) * (K / 2) +
+                                     64 * gi + 16 * q);
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxGpw / 4; ++i) {  // group g0 + 4 i + q
+        const int gi = g0 + (4 * i + q < ng ? 4 * i + q : ng - 1);
+#pragma unroll
+        for (int h = 0; h < NH; ++h) sv[h][i] = a.ws[(row + h * N) * NG + gi];
+    }
+    // the direct-to-LDS loads (issued first) have landed: at most the weight
+    // loads remain in flight
+    constexpr int kWeightLoads = NH * (kMaxGpw + kMaxGpw / 4);
+    static_assert(kWeightLoads < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((kWeightLoads & 15) | ((kWeightLoads >> 4) << 14) | (7 << 4));
+    asm volatile("s_barrier" ::: "memory");
+
+    // 3. per group: two MFMAs (codes 32 q .. +15, then +16 .. +31 of the group)
+    const int m = c < MT ? c : MT - 1;  // token of this lane's activation operand
+    const unsigned char* xr = xq_lds + m * K + 16 * 2 * q;
+#pragma unroll
+    for (int i = 0; i < kMaxGpw; ++i) {
+        if (i >= ng) continue;
+        const int g = g0 + i;
+        const v4i a0 = *reinterpret_cast<const v4i*>(xr + 128 * g);
+        const v4i a1 = *reinterpret_cast<const v4i*>(xr + 128 * g + 16);
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            const v4i b0{(int)(wv[h][i].x & kNibbleMask), (int)((wv[h][i].x >> 4) & kNibbleMask),
+                         (int)(wv[h][i].y & kNibbleMask), (int)((wv[h][i].y >> 4) & kNibbleMask)};
+            const v4i b1{(int)(wv[h][i].z & kNibbleMask), (int)((wv[h][i].z >> 4) & kNibbleMask),
+                         (int)(wv[h][i].w & kNibbleMask), (int)((wv[h][i].w >> 4) & kNibbleMask)};
+            v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, v4i{0, 0, 0, 0}, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, d, 0, 0, 0);
+            // lane (row c, quarter q) holds tokens 4 q .. 4 q + 3
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int t = 4 * q + j;
+                if (t < MT) acc_lds[((t * NH + h) * RB + 16 * blk + c) * NGP + g] = d[j];
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxGpw / 4; ++i) {
+        const int gi = 4 * i + q;
+        if (gi < ng) {
+#pragma unroll
+            for (int h = 0; h < NH; ++h)
+                sm_lds[(h * RB + 16 * blk + c) * NGP + g0 + gi] = make_float2(f16lo(sv[h][i]), f16hi(sv[h][i]));
+        }
+    }
+    __syncthreads();
+
+    if (a.acc_dump) {  // test hook: the group sums exactly as the epilogue reads them
+        const int rows_total = NH * (int)N;
+        for (int i = tid; i < MT * NH * RB * NG; i += 256) {
+            const int ee = i % NG, rl = (i / NG) % RB, h = (i / (NG * RB)) % NH, t = i / (NG * RB * NH);
+            const int64_t rr = r0 + rl;
+            if (t < a.M && rr < N)
+                a.acc_dump[((int64_t)t * rows_total + h * N + rr) * NG + ee] = acc_lds[((t * NH + h) * RB + rl) * NGP + ee];
+        }
+    }
+
+    // 4. fp32 epilogue: one chain per (token, row) over the groups in order
+    auto chain = [&](int t, int h, int rl) -> float {
+        const int32_t* ar = acc_lds + ((t * NH + h) * RB + rl) * NGP;
+        const float2* sr = sm_lds + (h * RB + rl) * NGP;
+        const int32_t* xsr = xs_lds + t * NG;
+        float acc = 0.0f;
+        int ee = 0;
+        if ((NG & 3) == 0) {
+            for (; ee < NG; ee += 4) {
+                const int4 a4 = *reinterpret_cast<const int4*>(ar + ee);
+                const int4 xi = *reinterpret_cast<const int4*>(xsr + ee);
+                const float4 x4 = make_float4((float)xi.x, (float)xi.y, (float)xi.z, (float)xi.w);
+                const float4 w01 = *reinterpret_cast<const float4*>(sr + ee);
+                const float4 w23 = *reinterpret_cast<const float4*>(sr + ee + 2);
+                acc = fmaf(w01.x, (float)a4.x, acc);
+                acc = fmaf(w01.y, x4.x, acc);
+                acc = fmaf(w01.z, (float)a4.y, acc);
+                acc = fmaf(w01.w, x4.y, acc);
+                acc = fmaf(w23.x, (float)a4.z, acc);
+                acc = fmaf(w23.y, x4.z, acc);
+                acc = fmaf(w23.z, (float)a4.w, acc);
+                acc = fmaf(w23.w, x4.w, acc);
+            }
+        }
+        for (; ee < NG; ++ee) {
+            const float2 w = sr[ee];
+            acc = fmaf(w.x, (float)ar[ee], acc);
+            acc = fmaf(w.y, (float)xsr[ee], acc);
+        }
+        return acc * dx_lds[t];
+    };
+    if (!ARGMAX) {
+        for (int o = tid; o < MT * RB; o += 256) {
+            const int t = o / RB, rl = o - t * RB;
+            const int64_t rr = r0 + rl;
+            if (t >= a.M || rr >= N) continue;
+            const float v = chain(t, 0, rl);
+            float* yo = a.y + (int64_t)t * N + rr;
+            if (MODE == 0) {
+                *yo = v;
+            } else if (MODE == 1) {
+                *yo = *yo + v;
+            } else {
+                *yo = silu_mul(v, chain(t, 1, rl));
+            }
+        }
+        return;
+    }
+
+    // fused greedy argmax, one key per (token, row), then the cross-workgroup combine
+    unsigned long long* keys = reinterpret_cast<unsigned long long*>(acc_lds);  // reused after a barrier
+    float vals[(MT * RB + 255) / 256];
+#pragma unroll
+    for (int k = 0; k < (MT * RB + 255) / 256; ++k) {
+        const int o = tid + 256 * k;
+        const int t = o / RB, rl = o - t * RB;
+        vals[k] = (o < MT * RB && t < a.M && r0 + rl < N) ? chain(t, 0, rl) : -3.4e38f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < (MT * RB + 255) / 256; ++k) {
+        const int o = tid + 256 * k;
+        if (o >= MT * RB) break;
+        const int t = o / RB, rl = o - t * RB;
+        const int64_t rr = r0 + rl;
+        unsigned long long key = 0;
+        if (t < a.M && rr < N) {
+            if (a.y) a.y[(int64_t)t * N + rr] = vals[k];
+            if (vals[k] > -3.0e38f) key = argmax_key(vals[k], (uint32_t)rr);
+        }
+        keys[o] = key;
+    }
+    __syncthreads();
+    unsigned long long best = 0;
+    if (tid < MT && tid < a.M)
+        for (int rl = 0; rl < RB; ++rl) best = keys[tid * RB + rl] > best ? keys[tid * RB + rl] : best;
+    argmax_combine<MT>(p.am, (int)a.M, p.nblocks, best);
+}
+
+template <int MT, int MODE, bool ARGMAX>
+hipError_t launch_rbw(const MfmaGemvParams& gp, int rbw, size_t lds, unsigned grid, hipStream_t s) {
+    dim3 g(grid), b(256);
+    switch (rbw) {
+        case 4: hipLaunchKernelGGL((gemv_mfma_kernel<MT, MODE, 4, ARGMAX>), g, b, lds, s, gp); break;
+        case 2: hipLaunchKernelGGL((gemv_mfma_kernel<MT, MODE, 2, ARGMAX>), g, b, lds, s, gp); break;
+        default: hipLaunchKernelGGL((gemv_mfma_kernel<MT, MODE, 1, ARGMAX>), g, b, lds, s, gp); break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// Measured (8 tokens, K = 2048): 12.1 us against 18.9 us for the dot4 kernel
+// at N = 32768, but slower below ~16K rows, where staging the activations
+// per workgroup and the extra barrier are not amortised.
+bool gemv_mfma_fits(const LinearArgs& a) {
+    return a.GA == a.K && a.G == 128 && a.M >= 3 && a.M <= 8 && a.K <= 8192 && a.N >= 16384;
+}
+
+hipError_t launch_gemv_mfma(const LinearArgs& a, const ArgmaxArgs* am, hipStream_t s) {
+    MfmaGemvParams gp{};
+    gp.a = a;
+    if (am) gp.am = *am;
+    const int NG = (int)(a.K / 128);
+    // row blocks per workgroup (the rest of the 4 waves split K, <= 16 groups
+    // each): as many as K allows while the grid still covers the 256 CUs
+    int rbw = NG <= kMaxGpw ? 4 : NG <= 2 * kMaxGpw ? 2 : 1;
+    while (rbw > 1 && (a.N + 16 * rbw - 1) / (16 * rbw) < 256) rbw /= 2;
+    const int ksplit = kWaves / rbw;
+    gp.NG = NG;
+    gp.NGP = (NG + 4) & ~3;
+    gp.gpw = (NG + ksplit - 1) / ksplit;
+    const int rb = 16 * rbw, nh = a.mode == 2 ? 2 : 1, mt = 8;
+    const unsigned grid = (unsigned)((a.N + rb - 1) / rb);
+    gp.nblocks = (int)grid;
+    const size_t lds = (size_t)mt * nh * rb * gp.NGP * 4 + (size_t)nh * rb * gp.NGP * 8 +
+                       (size_t)((mt * NG + 63) & ~63) * 4 + 64 * 4 + (size_t)mt * a.K;
+    if (am) return launch_rbw<8, 0, true>(gp, rbw, lds, grid, s);
+    switch (a.mode) {
+        case 0: return launch_rbw<8, 0, false>(gp, rbw, lds, grid, s);
+        case 1: return launch_rbw<8, 1, false>(gp, rbw, lds, grid, s);
+        default: return launch_rbw<8, 2, false>(gp, rbw, lds, grid, s);
+    }
+}
+
+}  // namespace wq

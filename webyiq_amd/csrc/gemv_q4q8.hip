@@ -19,6 +19,7 @@
 // The fp32 epilogue then runs one fma chain per (token, row) over the groups
 // in index order, the order the CPU oracle restates, so outputs are
 // bit-reproducible (modes 0 and 1) and the fused argmax sees the same logits.
+#include "argmax_combine.hpp"
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -419,7 +420,6 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     // fused greedy argmax (argmax.wgsl:19-34 tie rule), one key per (t, row)
     unsigned long long* keys = reinterpret_cast<unsigned long long*>(
         (reinterpret_cast<uintptr_t>(dx_lds + (size_t)MT * NDX) + 7) & ~uintptr_t(7));
-    __shared__ unsigned int last_block;
     for (int o = tid; o < MT * RB; o += nthreads) {
         const int t = o / RB, rl = o - t * RB;
         const int64_t row = r0 + rl;
@@ -432,54 +432,10 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         keys[o] = key;
     }
     __syncthreads();
-    // Cross-workgroup combine without fences (a device-scope release would
-    // write back the XCD's L2): keys and tickets live in kArgmaxSlots cache
-    // lines; a workgroup's atomicMax returns before its ticket is taken, and
-    // both are device-coherent atomics, so a ticket implies the max landed.
-    // The last workgroup of each slot takes a top ticket; the last of those
-    // reduces the slots, writes the token and clears the workspace.
-    const int kslot = (int)(blockIdx.x % kArgmaxSlots);
-    if (tid < MT && tid < a.M) {
-        unsigned long long best = 0;
+    unsigned long long best = 0;
+    if (tid < MT && tid < a.M)
         for (int rl = 0; rl < RB; ++rl) best = keys[tid * RB + rl] > best ? keys[tid * RB + rl] : best;
-        const unsigned long long old = atomicMax(p.am.keys + kslot * kArgmaxSlotWords + tid, best);
-        asm volatile("" ::"v"(old));  // the returned value: this atomic has been performed
-    }
-    __syncthreads();
-    const int used = p.nblocks < kArgmaxSlots ? p.nblocks : kArgmaxSlots;
-    if (tid == 0) {
-        const unsigned in_slot = (unsigned)((p.nblocks - kslot + kArgmaxSlots - 1) / kArgmaxSlots);
-        unsigned int done = atomicAdd(p.am.ticket + kslot * kArgmaxSlotWords * 2, 1u);
-        bool last = false;
-        if (done == in_slot - 1) {
-            unsigned int top = atomicAdd(p.am.ticket + kArgmaxSlots * kArgmaxSlotWords * 2, 1u);
-            last = top == (unsigned)used - 1;
-        }
-        last_block = last;
-    }
-    __syncthreads();
-    if (last_block) {
-        // every slot key read at once (independent device-coherent loads),
-        // then reduced in LDS
-        __shared__ unsigned long long slot_keys[kArgmaxSlots * MT];
-        for (int o = tid; o < used * MT; o += nthreads)
-            slot_keys[o] = __hip_atomic_load(p.am.keys + (o / MT) * kArgmaxSlotWords + (o % MT), __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        if (tid < a.M) {
-            unsigned long long k = 0;
-            for (int sl = 0; sl < used; ++sl) k = slot_keys[sl * MT + tid] > k ? slot_keys[sl * MT + tid] : k;
-            uint32_t idx = k ? 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull) : 0u;
-            p.am.tok_out[tid] = p.am.ids ? p.am.ids[idx] : idx;
-        }
-        __syncthreads();
-        for (int o = tid; o < used * MT; o += nthreads)
-            __hip_atomic_store(p.am.keys + (o / MT) * kArgmaxSlotWords + (o % MT), 0ull, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        for (int o = tid; o <= used; o += nthreads)
-            __hip_atomic_store(p.am.ticket + (o < used ? o * kArgmaxSlotWords * 2 : kArgmaxSlots * kArgmaxSlotWords * 2),
-                               0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    argmax_combine<MT>(p.am, (int)a.M, p.nblocks, best);
 }
 
 // ------------------------------------------------------------ dispatch ----
@@ -600,6 +556,7 @@ GemvParams params_of(const LinearArgs& a, const Plan& pl) {
 }  // namespace
 
 hipError_t launch_gemv(const LinearArgs& a, hipStream_t s) {
+    if (gemv_mfma_fits(a)) return launch_gemv_mfma(a, nullptr, s);
     Plan pl = make_plan(a, false);
     GemvParams gp = params_of(a, pl);
     switch (a.mode) {
@@ -610,6 +567,7 @@ hipError_t launch_gemv(const LinearArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_lm_head_argmax(const LinearArgs& a, const ArgmaxArgs& am, hipStream_t s) {
+    if (gemv_mfma_fits(a)) return launch_gemv_mfma(a, &am, s);
     Plan pl = make_plan(a, true);
     GemvParams gp = params_of(a, pl);
     gp.am = am;

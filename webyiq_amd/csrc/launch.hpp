@@ -75,6 +75,10 @@ hipError_t launch_quant_act(const QuantArgs& a, hipStream_t s);
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t s);
 hipError_t launch_gather_rows(const GatherArgs& a, hipStream_t s);
 hipError_t launch_gemv(const LinearArgs& a, hipStream_t s);
+// 3..8 tokens, per-token activations, group 128, K <= 8192: the int8-MFMA
+// GEMV (am != nullptr: with the fused argmax)
+bool gemv_mfma_fits(const LinearArgs& a);
+hipError_t launch_gemv_mfma(const LinearArgs& a, const ArgmaxArgs* am, hipStream_t s);
 hipError_t launch_gemv_quant_in(const LinearArgs& a, const QuantInArgs& q, hipStream_t s);
 hipError_t launch_lm_head_argmax(const LinearArgs& a, const ArgmaxArgs& am, hipStream_t s);
 hipError_t launch_gemm(const LinearArgs& a, hipStream_t s);
