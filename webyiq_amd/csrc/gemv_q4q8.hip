@@ -41,6 +41,15 @@ struct GemvParams {
     int nblocks; // gridDim.x
 };
 
+// LDS pointer p rounded up to a multiple of A bytes, as an offset from the LDS
+// base: rounding the pointer as an integer loses its address space, and its
+// accesses become flat ones, which count (and wait) with the global loads.
+template <int A, typename T>
+__device__ __forceinline__ T* lds_align(unsigned char* base, const void* p) {
+    const size_t off = static_cast<size_t>(reinterpret_cast<const unsigned char*>(p) - base);
+    return reinterpret_cast<T*>(base + ((off + A - 1) & ~size_t(A - 1)));
+}
+
 template <int MT, int MODE, int G, bool PT, int IPW, bool ARGMAX, bool QIN>
 __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     constexpr int GE = PT ? G : 32;        // accumulation group
@@ -85,7 +94,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     float* dx_lds = xs_lds + (size_t)MT * NE;
     // fused quantiser scratch (QIN kernels have no argmax keys)
     static_assert(!(QIN && ARGMAX), "no fused quantiser in the lm_head kernel");
-    float* qin_lds = dx_lds + (size_t)MT * NDX;
+    float* qin_lds = lds_align<16, float>(smem, dx_lds + (size_t)MT * NDX);
 
     // Lanes past the end of a partial pass (K % 2048 != 0) load from position 0
     // and never write their results: every load below is unconditional, so no
@@ -105,23 +114,36 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     //    before the weight stream, so waiting for them does not wait for it.
     constexpr int QT = QIN ? MT : 1;
     float4 qx[QT][8], qw[8];
-    const int qus = 8 / p.nslots, qu0 = slot * qus;
+    const int qus = 8 / p.nslots, qu0 = slot * qus;  // nslots is 1, 2 or 4: qus 8, 4 or 2
+    // f(i) for this wave's loads i < qus; the skipped ones are branched over
+    // (uniformly), not computed and discarded
+    auto for_chunks = [&](auto&& f) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) f(i);
+        if (qus >= 4) {
+            asm volatile("");
+#pragma unroll
+            for (int i = 2; i < 4; ++i) f(i);
+        }
+        if (qus == 8) {
+            asm volatile("");
+#pragma unroll
+            for (int i = 4; i < 8; ++i) f(i);
+        }
+    };
     if constexpr (QIN) {
         const int nchunk = K / 4;
         const float* nsrc = p.qin.norm_w ? p.qin.norm_w : p.qin.x;  // unconditional loads
+        for_chunks([&](int i) {
+            const int c = 512 * j + 64 * (qu0 + i) + lane;
+            const int cc = c < nchunk ? c : 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            if (i < qus) {
-                const int c = 512 * j + 64 * (qu0 + i) + lane;
-                const int cc = c < nchunk ? c : 0;
-#pragma unroll
-                for (int t = 0; t < MT; ++t) {
-                    const int64_t tt = t < a.M ? t : a.M - 1;
-                    qx[t][i] = reinterpret_cast<const float4*>(p.qin.x + tt * a.K)[cc];
-                }
-                qw[i] = reinterpret_cast<const float4*>(nsrc)[cc];
+            for (int t = 0; t < MT; ++t) {
+                const int64_t tt = t < a.M ? t : a.M - 1;
+                qx[t][i] = reinterpret_cast<const float4*>(p.qin.x + tt * a.K)[cc];
             }
-        }
+            qw[i] = reinterpret_cast<const float4*>(nsrc)[cc];
+        });
         // keep these loads ahead of the weight stream (no sinking into their
         // use, which would wait for every weight load)
         asm volatile("" ::: "memory");
@@ -172,17 +194,15 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         float* red = qin_lds;                 // [MT][8] pass sums of squares
         float* wmax = qin_lds + MT * 8;       // [MT][8] absmax per wave
         float* sub = qin_lds + MT * 16;       // [MT][8 waves][64] lane subtrees
-        uint32_t* codes = reinterpret_cast<uint32_t*>(  // [MT][K/4], 16-byte aligned
-            (reinterpret_cast<uintptr_t>(sub + MT * 8 * 64) + 15) & ~uintptr_t(15));
+        uint32_t* codes = lds_align<16, uint32_t>(smem, sub + MT * 8 * 64);  // [MT][K/4]
         const int nchunk = K / 4;
         const int nsl = p.nslots;
-        auto valid = [&](int i) { return i < qus && 512 * j + 64 * (qu0 + i) + lane < nchunk; };
+        auto valid = [&](int i) { return 512 * j + 64 * (qu0 + i) + lane < nchunk; };  // partial pass
         if (p.qin.norm_w) {
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
                 float c[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) c[i] = valid(i) ? chunk_ss(qx[t][i]) : 0.0f;
+                for_chunks([&](int i) { c[i] = valid(i) ? chunk_ss(qx[t][i]) : 0.0f; });
                 // this wave's subtree: 2, 4 or 8 of the lane's chunks
                 float st = c[0] + c[1];
                 if (qus >= 4) st = st + (c[2] + c[3]);
@@ -204,37 +224,44 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
             __syncthreads();
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
+                // pass sums in pass order (J <= 8; all 8 read at once)
+                const float4 ra = reinterpret_cast<const float4*>(red + t * 8)[0];
+                const float4 rb = reinterpret_cast<const float4*>(red + t * 8)[1];
+                const float rr[8] = {ra.x, ra.y, ra.z, ra.w, rb.x, rb.y, rb.z, rb.w};
                 float total = 0.0f;
-                for (int jj = 0; jj < p.J; ++jj) total = total + red[t * 8 + jj];
-                const float r = 1.0f / sqrt_rn(total / (float)K + p.qin.eps);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    if (i < qus) {
-                        qx[t][i].x = (qx[t][i].x * r) * qw[i].x;
-                        qx[t][i].y = (qx[t][i].y * r) * qw[i].y;
-                        qx[t][i].z = (qx[t][i].z * r) * qw[i].z;
-                        qx[t][i].w = (qx[t][i].w * r) * qw[i].w;
-                    }
-                }
+                for (int jj = 0; jj < 8; ++jj) total = jj < p.J ? total + rr[jj] : total;
+                const float r = 1.0f / sqrt_rn(total / (float)K + p.qin.eps);
+                for_chunks([&](int i) {
+                    qx[t][i].x = (qx[t][i].x * r) * qw[i].x;
+                    qx[t][i].y = (qx[t][i].y * r) * qw[i].y;
+                    qx[t][i].z = (qx[t][i].z * r) * qw[i].z;
+                    qx[t][i].w = (qx[t][i].w * r) * qw[i].w;
+                });
             }
         }
         // per-token absmax (order-free), dx = amax / 127
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
             float mx = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for_chunks([&](int i) {
                 if (valid(i))
                     mx = fmaxf(mx, fmaxf(fmaxf(fabsf(qx[t][i].x), fabsf(qx[t][i].y)),
                                          fmaxf(fabsf(qx[t][i].z), fabsf(qx[t][i].w))));
+            });
             mx = wave_max(mx);
             if (lane == 0) wmax[t * 8 + wave] = mx;
         }
         __syncthreads();
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-            float amax = wmax[t * 8];
-            for (int w = 1; w < NW; ++w) amax = fmaxf(amax, wmax[t * 8 + w]);
+            // NW <= 8 waves; all 8 read at once
+            const float4 ma = reinterpret_cast<const float4*>(wmax + t * 8)[0];
+            const float4 mb = reinterpret_cast<const float4*>(wmax + t * 8)[1];
+            const float mm[8] = {ma.x, ma.y, ma.z, ma.w, mb.x, mb.y, mb.z, mb.w};
+            float amax = mm[0];
+#pragma unroll
+            for (int w = 1; w < 8; ++w) amax = w < NW ? fmaxf(amax, mm[w]) : amax;
             dxv[t] = amax / 127.0f;
         }
         // codes of this wave's chunks -> LDS (and, from workgroup 0, to memory)
@@ -242,9 +269,8 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         for (int t = 0; t < MT; ++t) {
             const float d = dxv[t], rd = 1.0f / d;
             const int64_t tt = t < a.M ? t : a.M - 1;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                if (!valid(i)) continue;
+            for_chunks([&](int i) {
+                if (!valid(i)) return;
                 const int c = 512 * j + 64 * (qu0 + i) + lane;
                 int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
                 if (d > 0.0f) {
@@ -257,7 +283,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
                                     ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)(q3 & 0xFF) << 24);
                 codes[t * nchunk + c] = wd;
                 if (blockIdx.x == 0 && t < a.M) reinterpret_cast<uint32_t*>(p.qin.xq + tt * a.K)[c] = wd;
-            }
+            });
         }
         __syncthreads();
         // this lane's 32 codes and its group's code sum
@@ -418,8 +444,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     }
 
     // fused greedy argmax (argmax.wgsl:19-34 tie rule), one key per (t, row)
-    unsigned long long* keys = reinterpret_cast<unsigned long long*>(
-        (reinterpret_cast<uintptr_t>(dx_lds + (size_t)MT * NDX) + 7) & ~uintptr_t(7));
+    unsigned long long* keys = lds_align<8, unsigned long long>(smem, dx_lds + (size_t)MT * NDX);
     for (int o = tid; o < MT * RB; o += nthreads) {
         const int t = o / RB, rl = o - t * RB;
         const int64_t row = r0 + rl;
@@ -482,11 +507,14 @@ Plan make_plan(const LinearArgs& a, bool argmax, bool qin = false) {
         size_t b = (size_t)p.MT * nh * rb * p.NEP * 4 + (size_t)nh * rb * (p.NG + 2) * 8 +
                    (size_t)p.MT * p.NE * 4 + (size_t)p.MT * (pt ? 1 : a.K / 32) * 4;
         if (argmax) b += 16 + (size_t)p.MT * rb * 8;
-        if (qin) b += (size_t)p.MT * (16 * 4 + 8 * 64 * 4 + a.K) + 16;
+        if (qin) b += (size_t)p.MT * (16 * 4 + 8 * 64 * 4 + a.K) + 32;
         return b;
     };
     // registers: weights in flight (4 per row half) + activations (8 per token)
-    auto regs_of = [&](int ipw_) { return nh * ipw_ * 4 + 8 * p.MT; };
+    // (the fused quantiser also holds its f32 input and norm weight: 4 per load)
+    auto regs_of = [&](int ipw_) {
+        return nh * ipw_ * 4 + 8 * p.MT + (qin ? 4 * (8 / p.nslots) * (p.MT + 1) : 0);
+    };
     while (ipw > 1 && (lds_of(ipw) > 65536 || regs_of(ipw) > 96))
         ipw = ipw == 8 ? 6 : ipw == 6 ? 4 : ipw / 2;
     p.IPW = ipw;
