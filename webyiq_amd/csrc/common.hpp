@@ -174,6 +174,13 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) 
 // within one ulp, and the candidate with the smallest |x - c^2| (exact in
 // double: c^2 has 48 significant bits) is the rounded root (a square root is
 // never exactly halfway between two floats).
+// total / K (IEEE).  For K a power of two it is the product with 2^-n,
+// rounded once like the quotient, so the same value without a division.
+__device__ __forceinline__ float mean_of(float total, int K) {
+    if ((K & (K - 1)) == 0) return total * __int_as_float((127 - __builtin_ctz(K)) << 23);
+    return total / (float)K;
+}
+
 __device__ float sqrt_rn(float x) {
     float y = __builtin_amdgcn_sqrtf(x);
     if (!(x > 0.0f) || isinf(x) || !(y > 0.0f)) return y;

@@ -188,10 +188,10 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         // fmaf chains, a pairwise tree over a lane's 8 chunks -- here split
         // over the waves of the pass and completed through LDS -- a pairwise
         // tree over the lanes, pass sums in pass order), so codes, scales and
-        // sums are bit-identical to wq_quant_act's.  Each wave quantises its
-        // own chunks into LDS; every wave then reads its lane's 32 codes.
+        // sums are bit-identical to wq_quant_act's.  Every wave completes
+        // every pass's tree itself (no second exchange).  Each wave quantises
+        // its own chunks into LDS; every wave then reads its lane's 32 codes.
         static_assert(!QIN || (PT && MT <= 2), "the fused quantiser is per token, M <= 2");
-        float* red = qin_lds;                 // [MT][8] pass sums of squares
         float* wmax = qin_lds + MT * 8;       // [MT][8] absmax per wave
         float* sub = qin_lds + MT * 16;       // [MT][8 waves][64] lane subtrees
         uint32_t* codes = lds_align<16, uint32_t>(smem, sub + MT * 8 * 64);  // [MT][K/4]
@@ -210,28 +210,22 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
                 sub[(t * 8 + wave) * 64 + lane] = st;
             }
             __syncthreads();
-            if (slot == 0) {
-#pragma unroll
-                for (int t = 0; t < MT; ++t) {
-                    const float* sp = sub + (t * 8 + j) * 64 + lane;  // slot s at wave s * J + j
-                    float pl = sp[0];
-                    if (nsl == 2) pl = pl + sp[p.J * 64];
-                    if (nsl == 4) pl = (pl + sp[64]) + (sp[128] + sp[192]);  // J == 1
-                    pl = wave_sum_tree(pl);
-                    if (lane == 0) red[t * 8 + j] = pl;
-                }
-            }
-            __syncthreads();
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
-                // pass sums in pass order (J <= 8; all 8 read at once)
-                const float4 ra = reinterpret_cast<const float4*>(red + t * 8)[0];
-                const float4 rb = reinterpret_cast<const float4*>(red + t * 8)[1];
-                const float rr[8] = {ra.x, ra.y, ra.z, ra.w, rb.x, rb.y, rb.z, rb.w};
+                // pass jj's lane partials: slot s's subtree sits at wave s * J + jj;
+                // the pass sums are added in pass order (J <= 8)
                 float total = 0.0f;
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) total = jj < p.J ? total + rr[jj] : total;
-                const float r = 1.0f / sqrt_rn(total / (float)K + p.qin.eps);
+                for (int jj = 0; jj < 8; ++jj) {
+                    if (jj < p.J) {
+                        const float* sp = sub + (t * 8 + jj) * 64 + lane;
+                        float pl = sp[0];
+                        if (nsl == 2) pl = pl + sp[p.J * 64];
+                        if (nsl == 4) pl = (pl + sp[64]) + (sp[128] + sp[192]);  // J == 1
+                        total = total + wave_sum_tree(pl);
+                    }
+                }
+                const float r = 1.0f / sqrt_rn(mean_of(total, K) + p.qin.eps);
                 for_chunks([&](int i) {
                     qx[t][i].x = (qx[t][i].x * r) * qw[i].x;
                     qx[t][i].y = (qx[t][i].y * r) * qw[i].y;
@@ -272,15 +266,8 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
             for_chunks([&](int i) {
                 if (!valid(i)) return;
                 const int c = 512 * j + 64 * (qu0 + i) + lane;
-                int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
-                if (d > 0.0f) {
-                    q0 = quant_code(qx[t][i].x, d, rd);
-                    q1 = quant_code(qx[t][i].y, d, rd);
-                    q2 = quant_code(qx[t][i].z, d, rd);
-                    q3 = quant_code(qx[t][i].w, d, rd);
-                }
-                const uint32_t wd = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) |
-                                    ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)(q3 & 0xFF) << 24);
+                const uint32_t wd =
+                    d > 0.0f ? quant_word(qx[t][i].x, qx[t][i].y, qx[t][i].z, qx[t][i].w, d, rd) : 0u;
                 codes[t * nchunk + c] = wd;
                 if (blockIdx.x == 0 && t < a.M) reinterpret_cast<uint32_t*>(p.qin.xq + tt * a.K)[c] = wd;
             });

@@ -47,16 +47,9 @@ __device__ __forceinline__ float absmax4(float4 v) {
 }
 
 __device__ __forceinline__ uint32_t pack_codes(float4 v, float d, float rd, int& sum) {
-    int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
-    if (d > 0.0f) {
-        q0 = quant_code(v.x, d, rd);
-        q1 = quant_code(v.y, d, rd);
-        q2 = quant_code(v.z, d, rd);
-        q3 = quant_code(v.w, d, rd);
-    }
-    sum = q0 + q1 + q2 + q3;
-    return (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
-           ((uint32_t)(q3 & 0xFF) << 24);
+    const uint32_t w = d > 0.0f ? quant_word(v.x, v.y, v.z, v.w, d, rd) : 0u;
+    sum = dot4(w, 0x01010101u, 0);
+    return w;
 }
 
 // Codes, per-32 scales and group sums of one load (64 consecutive chunks
@@ -130,7 +123,7 @@ __global__ __launch_bounds__(kQuantThreads) void quant_split_kernel(QuantArgs a)
         __syncthreads();
         float total = 0.0f;
         for (int j = 0; j < J; ++j) total = total + red[j];
-        r = 1.0f / sqrt_rn(total / (float)K + a.eps);
+        r = 1.0f / sqrt_rn(mean_of(total, K) + a.eps);
     }
 
     float dtok = 0.0f;
@@ -225,7 +218,7 @@ __global__ __launch_bounds__(kQuantThreads) void quant_wave_kernel(QuantArgs a) 
             const float p = ((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]));
             total = total + wave_sum_tree(p);
         });
-        r = 1.0f / sqrt_rn(total / (float)K + a.eps);
+        r = 1.0f / sqrt_rn(mean_of(total, K) + a.eps);
     }
     auto load = [&](int j, int u) -> float4 { return NORM ? normed(raw(j, u), r, nwt(j, u)) : raw(j, u); };
 
