@@ -186,6 +186,37 @@ int wq_gather_rows(void* stream, const uint32_t* sq, const uint32_t* ss, int64_t
                    int32_t G, const uint32_t* ids, int64_t R, uint32_t* dq, uint32_t* ds);
 
 /*
+ * MTP input stage: the int8 input of the MTP fc projection, a [M, 2K] row
+ * per token with per-32 activation scales (GA = 32, Ge = 32):
+ *   columns [0, K)  = quant(norm_e(emb[m])),
+ *   columns [K, 2K) = quant(norm_h(norm_f(x[m]))),
+ * each norm v * (r * w) with r = 1 / sqrt(mean(v^2) + eps) over the values it
+ * normalises (mtp_in.wgsl:45-89, dispatched by graph.rs:500-504; emb is the
+ * embedding of the next token, x the last hidden state before the final
+ * norm).  xq i8 [M, 2K], dx f32 [M, 2K/32], xs i32 [M, 2K/32];
+ * K % 128 == 0; emb, x, the norms and xq 16-byte aligned.
+ */
+int wq_mtp_in(void* stream, const float* emb, const float* x, const float* norm_f,
+              const float* norm_e, const float* norm_h, float eps, int64_t M, int64_t K,
+              int8_t* xq, float* dx, int32_t* xs);
+
+/*
+ * Flash-decoding merge of attention partials, emitted as the int8 input of
+ * the o projection with per-32 activation scales (attn_combine.wgsl:1-83,
+ * dispatched per (token, head) by graph.rs:289-291).  part f32
+ * [M, H, nch, D + 2]: per chunk of 32 positions the D weighted output sums,
+ * the chunk's maximum score and its weight sum (attn.wgsl:104-113).  Token
+ * m covers positions 0 ..= pos + m.  gate (nullable, Qwen3.5's gated
+ * attention): the gate of (m, h, i) is gate[m * gate_stride + h * 2D + D + i]
+ * and the output is divided by 1 + exp(-gate).  xq i8 [M, H*D],
+ * dx f32 [M, H*D/32], xs i32 [M, H*D/32]; D in {64, 128, 256},
+ * nch <= 4096, pos + M - 1 < 32 nch; xq 16-byte aligned.
+ */
+int wq_attn_combine(void* stream, const float* part, int64_t M, int64_t H, int64_t D,
+                    int64_t nch, int64_t pos, const float* gate, int64_t gate_stride,
+                    int8_t* xq, float* dx, int32_t* xs);
+
+/*
  * Test hooks: wq_gemv / wq_gemm that also store the exact int32 group sums
  * A[t, row, e] = sum over group e of q[row, k] * xq[t, k] that the kernel
  * folded into y, into acc i32 [M, rows, K/Ge] (rows = N, or 2N in

@@ -45,6 +45,8 @@ def lib():
         L.or_argmax.argtypes = [P, i64, i64, P, P]
         L.or_embed.argtypes = [P, P, i64, i64, i32, P, i64, P]
         L.or_gather_rows.argtypes = [P, P, i64, i64, i32, P, i64, P, P]
+        L.or_mtp_in.argtypes = [P, P, P, P, P, ctypes.c_float, i64, i64, P, P, P]
+        L.or_attn_combine.argtypes = [P, i64, i64, i64, i64, i64, P, i64, P, P, P]
         _lib = L
     return _lib
 
@@ -182,3 +184,30 @@ def gather_rows(wq, ws, K, G, ids):
     ds = np.empty((ids.size, K // G), np.uint32)
     lib().or_gather_rows(_p(wq), _p(ws), wq.shape[0], K, G, _p(ids), ids.size, _p(dq), _p(ds))
     return dq, ds
+
+
+def mtp_in(emb, x, nf, ne, nh, eps=1e-6):
+    """MTP input stage -> (xq i8 [M, 2K], dx f32 [M, 2K/32], xs i32 [M, 2K/32])."""
+    emb = _c(np.atleast_2d(emb), np.float32)
+    x = _c(np.atleast_2d(x), np.float32)
+    M, K = x.shape
+    xq = np.empty((M, 2 * K), np.int8)
+    dx = np.empty((M, 2 * K // 32), np.float32)
+    xs = np.empty((M, 2 * K // 32), np.int32)
+    nf, ne, nh = (_c(a, np.float32) for a in (nf, ne, nh))
+    lib().or_mtp_in(_p(emb), _p(x), _p(nf), _p(ne), _p(nh), ctypes.c_float(eps), M, K, _p(xq), _p(dx), _p(xs))
+    return xq, dx, xs
+
+
+def attn_combine(part, pos, gate=None, gate_stride=0):
+    """Chunk merge + per-32 quant -> (xq i8 [M, H*D], dx f32 [M, H*D/32], xs i32 [M, H*D/32])."""
+    part = _c(part, np.float32)
+    M, H, nch, D2 = part.shape
+    D = D2 - 2
+    K = H * D
+    xq = np.empty((M, K), np.int8)
+    dx = np.empty((M, K // 32), np.float32)
+    xs = np.empty((M, K // 32), np.int32)
+    g = None if gate is None else _c(gate, np.float32)
+    lib().or_attn_combine(_p(part), M, H, D, nch, int(pos), _p(g), int(gate_stride), _p(xq), _p(dx), _p(xs))
+    return xq, dx, xs

@@ -363,3 +363,98 @@ void or_gather_rows(const uint32_t* sq, const uint32_t* ss, int64_t V, int64_t K
         for (int64_t i = 0; i < WS; ++i) ds[r * WS + i] = ok ? ss[(int64_t)src * WS + i] : 0u;
     }
 }
+
+/* ------------------------------------------------------------ MTP input ---- */
+
+/* mtp_in.wgsl:45-89 (dispatch graph.rs:500-504): row m of the [M, 2K] output
+ * is quant32(norm_e(emb[m])) then quant32(norm_h(norm_f(x[m]))).  Each norm
+ * scales as the reference writes it, v * (r * w) (mtp_in.wgsl:56,65,70), with
+ * r = 1 / sqrt(mean(v^2) + eps) from rms_scale's order over the values it
+ * normalises; quant32 is or_quant_act's per-32 quantiser (GA = Ge = 32). */
+void or_mtp_in(const float* emb, const float* x, const float* nf, const float* ne,
+               const float* nh, float eps, int64_t M, int64_t K,
+               int8_t* xq, float* dx, int32_t* xs) {
+    float* v = (float*)malloc((size_t)K * 4);
+    for (int64_t m = 0; m < M; ++m) {
+        for (int half = 0; half < 2; ++half) {
+            const int64_t row = 2 * m + half;
+            memcpy(v, (half ? x : emb) + m * K, (size_t)K * 4);
+            const float* w0 = half ? nf : ne;
+            float r = rms_scale(v, K, eps);
+            for (int64_t k = 0; k < K; ++k) v[k] = v[k] * (r * w0[k]);
+            if (half) {
+                r = rms_scale(v, K, eps);
+                for (int64_t k = 0; k < K; ++k) v[k] = v[k] * (r * nh[k]);
+            }
+            or_quant_act(v, NULL, eps, 1, K, 32, 32, xq + row * K, dx + row * (K / 32),
+                         xs + row * (K / 32));
+        }
+    }
+    free(v);
+}
+
+/* ------------------------------------------------ attention chunk merge ---- */
+
+/* attn_combine.wgsl:36-82 (dispatch graph.rs:289-291) in the HIP kernel's
+ * order.  part [M, H, nch, D + 2]: per chunk the D output sums, the chunk
+ * max score and its weight sum (attn.wgsl:104-113); token m merges chunks
+ * 0 .. (pos + m + 32) / 32 - 1.
+ *   mx = max m_c; w_c = expf(m_c - mx)
+ *   l: lane j (0..63) accumulates fmaf(w_c, l_c, .) over c = j, j + 64, ...,
+ *      then the pairwise tree over the 64 lanes (as rms_scale)
+ *   o[i] = (fmaf chain of w_c * part_c[i] over c in order) / l
+ *   gated: o[i] = o[i] / (1 + expf(-g[i])), g at gate[m*gs + h*2D + D + i]
+ *   per 32 dims: dx = amax / 127, xq = rint(o / dx), xs = sum xq.
+ * The device's expf may differ from the host's in the last bit, so codes
+ * are exact only where every weight is exp(0) (equal chunk maxima) and no
+ * gate is applied; elsewhere the comparison carries a tolerance. */
+void or_attn_combine(const float* part, int64_t M, int64_t H, int64_t D, int64_t nch,
+                     int64_t pos, const float* gate, int64_t gs,
+                     int8_t* xq, float* dx, int32_t* xs) {
+    float* w = (float*)malloc((size_t)nch * 4);
+    float* o = (float*)malloc((size_t)D * 4);
+    const int64_t K = H * D;
+    for (int64_t m = 0; m < M; ++m) {
+        const int64_t n = (pos + m + 32) / 32;
+        for (int64_t h = 0; h < H; ++h) {
+            const float* hb = part + ((m * H + h) * nch) * (D + 2);
+            float mx = -3.0e38f;
+            for (int64_t c = 0; c < n; ++c) mx = fmaxf(mx, hb[c * (D + 2) + D]);
+            float p[64];
+            for (int j = 0; j < 64; ++j) p[j] = 0.0f;
+            for (int64_t c = 0; c < n; ++c) {
+                w[c] = expf(hb[c * (D + 2) + D] - mx);
+                p[c % 64] = fmaf(w[c], hb[c * (D + 2) + D + 1], p[c % 64]);
+            }
+            for (int off = 1; off < 64; off <<= 1)
+                for (int j = 0; j < 64; ++j)
+                    if (!(j & off)) p[j] = p[j] + p[j + off];
+            const float l = p[0];
+            for (int64_t i = 0; i < D; ++i) {
+                float acc = 0.0f;
+                for (int64_t c = 0; c < n; ++c) acc = fmaf(w[c], hb[c * (D + 2) + i], acc);
+                o[i] = acc / l;
+                if (gate) o[i] = o[i] / (1.0f + expf(-gate[m * gs + h * 2 * D + D + i]));
+            }
+            for (int64_t g = 0; g < D / 32; ++g) {
+                float amax = 0.0f;
+                for (int i = 0; i < 32; ++i) {
+                    const float e = fabsf(o[32 * g + i]);
+                    if (e > amax) amax = e;
+                }
+                const float d = amax / 127.0f;
+                int32_t sum = 0;
+                for (int i = 0; i < 32; ++i) {
+                    const float q = d > 0.0f ? rintf(o[32 * g + i] / d) : 0.0f;
+                    xq[m * K + h * D + 32 * g + i] = (int8_t)q;
+                    sum += (int32_t)q;
+                }
+                const int64_t gi = m * (K / 32) + (h * D + 32 * g) / 32;
+                dx[gi] = d;
+                xs[gi] = sum;
+            }
+        }
+    }
+    free(w);
+    free(o);
+}

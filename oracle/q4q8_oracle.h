@@ -71,6 +71,17 @@ void or_embed(const uint32_t* eq, const uint32_t* es, int64_t V, int64_t K, int 
 void or_gather_rows(const uint32_t* sq, const uint32_t* ss, int64_t V, int64_t K, int G,
                     const uint32_t* ids, int64_t R, uint32_t* dq, uint32_t* ds);
 
+/* MTP input stage (mtp_in.wgsl:45-89): xq i8 [M, 2K], dx/xs [M, 2K/32]. */
+void or_mtp_in(const float* emb, const float* x, const float* nf, const float* ne,
+               const float* nh, float eps, int64_t M, int64_t K,
+               int8_t* xq, float* dx, int32_t* xs);
+
+/* Flash-decoding chunk merge + per-32 int8 groups (attn_combine.wgsl:36-82):
+ * xq i8 [M, H*D], dx/xs [M, H*D/32]; gate nullable (row stride gs). */
+void or_attn_combine(const float* part, int64_t M, int64_t H, int64_t D, int64_t nch,
+                     int64_t pos, const float* gate, int64_t gs,
+                     int8_t* xq, float* dx, int32_t* xs);
+
 #ifdef __cplusplus
 }
 #endif

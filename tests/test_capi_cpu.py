@@ -21,7 +21,7 @@ def declared_symbols():
 
 def test_exports_every_declared_symbol():
     names = declared_symbols()
-    assert len(names) == 15
+    assert len(names) == 17
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(_lib.PROTOTYPES)
@@ -131,3 +131,33 @@ def test_embed_and_gather_errors():
     assert g(None, A16, A4, 100, 2048, 128, None, 4, A16, A4) == _lib.WQ_EINVAL
     assert g(None, A16, A4, 100, 2048, 128, A4, 0, A16, A4) == _lib.WQ_ESHAPE
     assert g(None, A16, A4, 100, 2048, 128, A4, 4, A4, A4) == _lib.WQ_EALIGN
+
+
+def mtp_in(*, emb=A16, x=A16, nf=A16, ne=A16, nh=A16, eps=1e-6, M=1, K=2048, xq=A16, dx=A4, xs=A4):
+    return L.wq_mtp_in(None, emb, x, nf, ne, nh, eps, M, K, xq, dx, xs)
+
+
+def test_mtp_in_argument_errors():
+    assert mtp_in(nh=None) == _lib.WQ_EINVAL and "norm_h is NULL" in err()
+    assert mtp_in(K=2000) == _lib.WQ_ESHAPE and "multiple of 128" in err()
+    assert mtp_in(M=0) == _lib.WQ_ESHAPE
+    assert mtp_in(eps=-1.0) == _lib.WQ_EINVAL and "eps" in err()
+    assert mtp_in(emb=A4) == _lib.WQ_EALIGN and "emb not 16-byte" in err()
+    assert mtp_in(xq=ctypes.c_void_p(0x10008)) == _lib.WQ_EALIGN
+
+
+def combine(*, part=A4, M=1, H=16, D=128, nch=128, pos=0, gate=None, gs=0, xq=A16, dx=A4, xs=A4):
+    return L.wq_attn_combine(None, part, M, H, D, nch, pos, gate, gs, xq, dx, xs)
+
+
+def test_attn_combine_argument_errors():
+    assert combine(part=None) == _lib.WQ_EINVAL and "part is NULL" in err()
+    assert combine(D=96) == _lib.WQ_ESHAPE and "head dim" in err()
+    assert combine(M=0) == _lib.WQ_ESHAPE and combine(H=0) == _lib.WQ_ESHAPE
+    assert combine(nch=4097) == _lib.WQ_ESHAPE and "chunks" in err()
+    assert combine(nch=4, pos=128) == _lib.WQ_ESHAPE and "context" in err()
+    assert combine(nch=4, pos=126, M=3) == _lib.WQ_ESHAPE     # token 2 at position 128
+    assert combine(pos=-1) == _lib.WQ_ESHAPE
+    assert combine(gate=A4, gs=2 * 16 * 128 - 1) == _lib.WQ_ESHAPE and "gate_stride" in err()
+    assert combine(xq=ctypes.c_void_p(0x10008)) == _lib.WQ_EALIGN
+    assert combine(part=ctypes.c_void_p(0x10002)) == _lib.WQ_EALIGN

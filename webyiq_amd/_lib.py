@@ -45,6 +45,8 @@ PROTOTYPES = {
     "wq_workspace_clear": ([_P, _P, _SZ], ctypes.c_int),
     "wq_embed": ([_P, _P, _P, _I64, _I64, _I32, _P, _I64, _P], ctypes.c_int),
     "wq_gather_rows": ([_P, _P, _P, _I64, _I64, _I32, _P, _I64, _P, _P], ctypes.c_int),
+    "wq_mtp_in": ([_P, _P, _P, _P, _P, _P, _F, _I64, _I64, _P, _P, _P], ctypes.c_int),
+    "wq_attn_combine": ([_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _P], ctypes.c_int),
 }
 
 

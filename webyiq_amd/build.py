@@ -22,7 +22,8 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libwebyiq_q4q8.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["capi.hip", "quant_act.hip", "gemv_q4q8.hip", "gemv_mfma.hip", "gemm_q4q8.hip", "argmax.hip", "embed.hip"]
+SOURCES = ["capi.hip", "quant_act.hip", "gemv_q4q8.hip", "gemv_mfma.hip", "gemm_q4q8.hip", "argmax.hip", "embed.hip",
+           "attn_combine.hip"]
 CFLAGS = [
     "--offload-arch=gfx950",
     "-O3",

@@ -303,6 +303,65 @@ int wq_gather_rows(void* stream, const uint32_t* sq, const uint32_t* ss, int64_t
     return hip_status(wq::launch_gather_rows(a, static_cast<hipStream_t>(stream)), fn);
 }
 
+int wq_mtp_in(void* stream, const float* emb, const float* x, const float* norm_f,
+              const float* norm_e, const float* norm_h, float eps, int64_t M, int64_t K, int8_t* xq,
+              float* dx, int32_t* xs) {
+    const char* fn = "wq_mtp_in";
+    REQUIRE_PTR(emb);
+    REQUIRE_PTR(x);
+    REQUIRE_PTR(norm_f);
+    REQUIRE_PTR(norm_e);
+    REQUIRE_PTR(norm_h);
+    REQUIRE_PTR(xq);
+    REQUIRE_PTR(dx);
+    REQUIRE_PTR(xs);
+    if (M < 1 || M > (int64_t(1) << 29))
+        return fail(WQ_ESHAPE, "%s: M = %lld out of range", fn, (long long)M);
+    if (K < 128 || K % 128 != 0 || K > (int64_t(1) << 24))
+        return fail(WQ_ESHAPE, "%s: K = %lld must be a positive multiple of 128", fn, (long long)K);
+    if (!(eps >= 0.0f)) return fail(WQ_EINVAL, "%s: eps must be >= 0", fn);
+    REQUIRE_ALIGN(emb, 16);
+    REQUIRE_ALIGN(x, 16);
+    REQUIRE_ALIGN(norm_f, 16);
+    REQUIRE_ALIGN(norm_e, 16);
+    REQUIRE_ALIGN(norm_h, 16);
+    REQUIRE_ALIGN(xq, 16);
+    REQUIRE_ALIGN(dx, 4);
+    REQUIRE_ALIGN(xs, 4);
+    wq::MtpInArgs a{emb, x, norm_f, norm_e, norm_h, eps, M, K, xq, dx, xs};
+    return hip_status(wq::launch_mtp_in(a, static_cast<hipStream_t>(stream)), fn);
+}
+
+int wq_attn_combine(void* stream, const float* part, int64_t M, int64_t H, int64_t D, int64_t nch,
+                    int64_t pos, const float* gate, int64_t gate_stride, int8_t* xq, float* dx,
+                    int32_t* xs) {
+    const char* fn = "wq_attn_combine";
+    REQUIRE_PTR(part);
+    REQUIRE_PTR(xq);
+    REQUIRE_PTR(dx);
+    REQUIRE_PTR(xs);
+    if (D != 64 && D != 128 && D != 256)
+        return fail(WQ_ESHAPE, "%s: head dim D = %lld (64, 128 or 256)", fn, (long long)D);
+    if (M < 1 || M > 64) return fail(WQ_ESHAPE, "%s: M = %lld tokens (1..64)", fn, (long long)M);
+    if (H < 1 || H > 1024) return fail(WQ_ESHAPE, "%s: H = %lld heads (1..1024)", fn, (long long)H);
+    if (nch < 1 || nch > wq::kCombineMaxChunks)
+        return fail(WQ_ESHAPE, "%s: nch = %lld chunks (1..%d)", fn, (long long)nch,
+                    wq::kCombineMaxChunks);
+    if (pos < 0 || pos + M - 1 >= 32 * nch)
+        return fail(WQ_ESHAPE, "%s: positions 0..%lld exceed the %lld-position context", fn,
+                    (long long)(pos + M - 1), (long long)(32 * nch));
+    if (gate && gate_stride < 2 * H * D)
+        return fail(WQ_ESHAPE, "%s: gate_stride = %lld < 2 H D = %lld", fn, (long long)gate_stride,
+                    (long long)(2 * H * D));
+    REQUIRE_ALIGN(part, 4);
+    if (gate) REQUIRE_ALIGN(gate, 4);
+    REQUIRE_ALIGN(xq, 16);
+    REQUIRE_ALIGN(dx, 4);
+    REQUIRE_ALIGN(xs, 4);
+    wq::AttnCombineArgs a{part, M, H, D, nch, pos, gate, gate_stride, xq, dx, xs};
+    return hip_status(wq::launch_attn_combine(a, static_cast<hipStream_t>(stream)), fn);
+}
+
 size_t wq_lm_head_workspace_bytes(void) { return wq::kArgmaxWorkspaceBytes; }
 
 int wq_workspace_clear(void* stream, void* workspace, size_t bytes) {

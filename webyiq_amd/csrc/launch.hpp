@@ -50,6 +50,36 @@ struct QuantInArgs {
     int32_t* xs;
 };
 
+// MTP input stage: per token m, row 2m = per-32 quant of norm_e(emb[m]) and
+// row 2m + 1 = per-32 quant of norm_h(norm_f(x[m])), each norm v * (r * w).
+struct MtpInArgs {
+    const float* emb;     // [M, K]
+    const float* x;       // [M, K]
+    const float* norm_f;  // [K] final norm
+    const float* norm_e;  // [K]
+    const float* norm_h;  // [K]
+    float eps;
+    int64_t M, K;
+    int8_t* xq;           // [M, 2K]
+    float* dx;            // [M, 2K/32]
+    int32_t* xs;          // [M, 2K/32]
+};
+
+// Flash-decoding merge of per-chunk attention partials, emitted as per-32
+// int8 groups for the o projection (nch <= kCombineMaxChunks: the chunk
+// weights of four wavefronts fit 64 KiB of LDS).
+constexpr int kCombineMaxChunks = 4096;
+struct AttnCombineArgs {
+    const float* part;    // [M, H, nch, D + 2]: chunk output sums, chunk max, chunk sum
+    int64_t M, H, D, nch;
+    int64_t pos;          // position of token 0; token m covers positions 0 ..= pos + m
+    const float* gate;    // nullable: gate of (m, h, i) at gate[m * gate_stride + h * 2D + D + i]
+    int64_t gate_stride;
+    int8_t* xq;           // [M, H * D]
+    float* dx;            // [M, H * D / 32]
+    int32_t* xs;          // [M, H * D / 32]
+};
+
 struct EmbedArgs {
     const uint32_t* q;    // [V, K/8] packed int4 rows
     const uint32_t* s;    // [V, K/G] (scale, min) words
@@ -72,6 +102,8 @@ struct GatherArgs {
 };
 
 hipError_t launch_quant_act(const QuantArgs& a, hipStream_t s);
+hipError_t launch_mtp_in(const MtpInArgs& a, hipStream_t s);
+hipError_t launch_attn_combine(const AttnCombineArgs& a, hipStream_t s);
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t s);
 hipError_t launch_gather_rows(const GatherArgs& a, hipStream_t s);
 hipError_t launch_gemv(const LinearArgs& a, hipStream_t s);

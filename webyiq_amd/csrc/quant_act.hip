@@ -243,6 +243,96 @@ __global__ __launch_bounds__(kQuantThreads) void quant_wave_kernel(QuantArgs a) 
     });
 }
 
+// MTP input stage (mtp_in.wgsl:45-89), one wavefront per (token, half), four
+// per workgroup, no barriers.  The norms scale as the reference does,
+// v * (r * w); their sums of squares run in this file's order (above), each
+// over the values it normalises.  Output row 2m + half of the [2M, K] view.
+template <int JC>
+__global__ __launch_bounds__(kQuantThreads) void mtp_in_kernel(MtpInArgs a) {
+    pin_arg(a.emb); pin_arg(a.x); pin_arg(a.norm_f); pin_arg(a.norm_e); pin_arg(a.norm_h);
+    pin_arg(a.eps); pin_arg(a.K); pin_arg(a.M); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
+    if (row >= 2 * a.M) return;  // whole wavefronts; the kernel has no barrier
+    const int64_t m = row >> 1;
+    const bool hidden = (row & 1) != 0;  // half 1: the hidden state
+    const int K = (int)a.K;
+    const int nchunk = K / 4;
+    const int J = (nchunk + kPassChunks - 1) / kPassChunks;
+    const float4* src = reinterpret_cast<const float4*>((hidden ? a.x : a.emb) + m * a.K);
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto chunk = [&](int j, int u) { return kPassChunks * j + 64 * u + lane; };
+
+    constexpr int NC = JC > 0 ? JC : 1;
+    float4 xc[NC][8];
+    if (JC > 0) {
+#pragma unroll
+        for (int j = 0; j < NC; ++j)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int c = chunk(j, u);
+                xc[j][u] = j < J && c < nchunk ? src[c] : zero4;
+            }
+    }
+    auto raw = [&](int j, int u) -> float4 {
+        if (JC > 0) return xc[JC > 0 ? j : 0][u];
+        const int c = chunk(j, u);
+        return c < nchunk ? src[c] : zero4;
+    };
+    auto weight = [&](const float* w, int j, int u) -> float4 {
+        const int c = chunk(j, u);
+        return c < nchunk ? reinterpret_cast<const float4*>(w)[c] : zero4;
+    };
+    auto scale = [](float4 v, float r, float4 w) {  // mtp_in.wgsl:56,65,70: v *= r * w
+        v.x = v.x * (r * w.x);
+        v.y = v.y * (r * w.y);
+        v.z = v.z * (r * w.z);
+        v.w = v.w * (r * w.w);
+        return v;
+    };
+    auto for_passes = [&](auto&& f) {
+        if constexpr (JC > 0) {
+#pragma unroll
+            for (int j = 0; j < NC; ++j)
+                if (j < J) f(j);
+        } else {
+            for (int j = 0; j < J; ++j) f(j);
+        }
+    };
+    // 1 / rms of the values vals(j, u) (mtp_in.wgsl:26-42)
+    auto inv_rms = [&](auto&& vals) {
+        float total = 0.0f;
+        for_passes([&](int j) {
+            float c[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) c[u] = chunk_ss(vals(j, u));
+            const float p = ((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]));
+            total = total + wave_sum_tree(p);
+        });
+        return 1.0f / sqrt_rn(mean_of(total, K) + a.eps);
+    };
+
+    const float r0 = inv_rms(raw);
+    const float* w0 = hidden ? a.norm_f : a.norm_e;
+    auto v0 = [&](int j, int u) { return scale(raw(j, u), r0, weight(w0, j, u)); };
+    float r1 = 0.0f;
+    if (hidden) r1 = inv_rms(v0);
+    auto out = [&](int j, int u) { return hidden ? scale(v0(j, u), r1, weight(a.norm_h, j, u)) : v0(j, u); };
+
+    QuantArgs q{};
+    q.K = a.K;
+    q.xq = a.xq;
+    q.dx = a.dx;
+    q.xs = a.xs;
+    for_passes([&](int j) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = chunk(j, u);
+            emit<false, 32>(q, row, c, c < nchunk, out(j, u), 0.0f, 0.0f, lane);
+        }
+    });
+}
+
 template <bool NORM, bool PT, int GE>
 hipError_t dispatch_rows(const QuantArgs& a, hipStream_t s) {
     const int64_t passes = (a.K + 4 * kPassChunks - 1) / (4 * kPassChunks);
@@ -273,6 +363,18 @@ hipError_t dispatch_format(const QuantArgs& a, hipStream_t s) {
 
 hipError_t launch_quant_act(const QuantArgs& a, hipStream_t s) {
     return a.norm_w ? dispatch_format<true>(a, s) : dispatch_format<false>(a, s);
+}
+
+hipError_t launch_mtp_in(const MtpInArgs& a, hipStream_t s) {
+    const int64_t passes = (a.K + 4 * kPassChunks - 1) / (4 * kPassChunks);
+    dim3 grid((unsigned)((2 * a.M + kQuantWaves - 1) / kQuantWaves)), block(kQuantThreads);
+    if (passes <= 1)
+        hipLaunchKernelGGL((mtp_in_kernel<1>), grid, block, 0, s, a);
+    else if (passes <= 3)
+        hipLaunchKernelGGL((mtp_in_kernel<3>), grid, block, 0, s, a);
+    else
+        hipLaunchKernelGGL((mtp_in_kernel<0>), grid, block, 0, s, a);
+    return hipGetLastError();
 }
 
 }  // namespace wq

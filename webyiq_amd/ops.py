@@ -209,6 +209,30 @@ def embed(w: Q4Tensor, tok, out=None, stream=None):
     return x
 
 
+def mtp_in(emb, x, norm_f, norm_e, norm_h, eps=1e-6, out: Optional[Acts] = None, stream=None) -> Acts:
+    """The MTP fc input (mtp_in.wgsl): per token, [quant(norm_e(emb)) |
+    quant(norm_h(norm_f(x)))] as one [M, 2K] row with per-32 scales."""
+    if emb.dim() == 1:
+        emb, x = emb[None], x[None]
+    M, K = x.shape
+    a = out if out is not None else empty_acts(M, 2 * K, GA=32, G=32, device=x.device)
+    _lib.call("wq_mtp_in", _stream(stream), _ptr(emb), _ptr(x), _ptr(norm_f), _ptr(norm_e), _ptr(norm_h),
+              float(eps), M, K, _ptr(a.xq), _ptr(a.dx), _ptr(a.xs))
+    return a
+
+
+def attn_combine(part, pos, gate=None, gate_stride=0, G=128, out: Optional[Acts] = None, stream=None) -> Acts:
+    """Merge flash-decoding partials part f32 [M, H, nch, D + 2] into the o
+    projection's int8 input (attn_combine.wgsl), per-32 scales; optional
+    Qwen3.5 gate rows (gate of head h at h*2D + D of a token's row)."""
+    M, H, nch, D2 = part.shape
+    D = D2 - 2
+    a = out if out is not None else empty_acts(M, H * D, GA=32, G=G, device=part.device)
+    _lib.call("wq_attn_combine", _stream(stream), _ptr(part), M, H, D, nch, int(pos), _ptr(gate),
+              int(gate_stride), _ptr(a.xq), _ptr(a.dx), _ptr(a.xs))
+    return a
+
+
 def gather_rows(w: Q4Tensor, ids, stream=None) -> Q4Tensor:
     """Packed rows ids of w as a new Q4Tensor (gather_rows.wgsl: the reduced
     draft lm_head)."""
