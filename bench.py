@@ -366,13 +366,50 @@ def bench_configs(torch, lib, ops):
         del ws
     res["cfg5_lm_head_argmax"] = head
 
+    # the other producers of int8 activations: the MTP input stage
+    # (mtp_in.wgsl, K = 2048) and the flash-decoding merge (attn_combine.wgsl,
+    # 16 heads of 128, 4096-position context); inputs L2/MALL-resident, as
+    # their producers just wrote them
+    prod = {}
+    Kh = 2048
+    for M in (1, 2):
+        emb = torch.randn((M, Kh), dtype=torch.float32, device="cuda")
+        xh = torch.randn((M, Kh), dtype=torch.float32, device="cuda")
+        nws = [torch.randn(Kh, dtype=torch.float32, device="cuda") for _ in range(3)]
+        a = ops.empty_acts(M, 2 * Kh, 32, 32)
+        ln = Launcher(lib, "wq_mtp_in", [P(emb.data_ptr()), P(xh.data_ptr())] + [P(t.data_ptr()) for t in nws] +
+                      [ctypes.c_float(1e-6), M, Kh, P(a.xq.data_ptr()), P(a.dx.data_ptr()), P(a.xs.data_ptr())])
+        graph_time(torch, [ln] * 32, 2)
+        t = graph_time(torch, [ln] * 32, 8)
+        nb = 4 * (2 * M * Kh + 3 * Kh) + 2 * M * Kh + 8 * (2 * M * Kh // 32)
+        prod[f"mtp_in_M{M}_K{Kh}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1)}
+    Hh, Dh, nch = 16, 128, 128
+    for M, pos in ((1, 511), (1, 4095 - 1), (2, 4094)):
+        parts = []
+        for _ in range(8):
+            pt = torch.randn((M, Hh, nch, Dh + 2), dtype=torch.float32, device="cuda")
+            pt[..., Dh + 1].uniform_(1.0, 32.0)
+            parts.append(pt)
+        a = ops.empty_acts(M, Hh * Dh, 32, G)
+        lns = [Launcher(lib, "wq_attn_combine", [P(pt.data_ptr()), M, Hh, Dh, nch, pos, None, 0,
+                                                 P(a.xq.data_ptr()), P(a.dx.data_ptr()), P(a.xs.data_ptr())])
+               for pt in parts]
+        graph_time(torch, lns, 2)
+        t = graph_time(torch, lns, 16)
+        nread = sum(Hh * ((pos + m + 32) // 32) * (Dh + 2) * 4 for m in range(M))
+        nb = nread + M * Hh * Dh + 8 * (M * Hh * Dh // 32)
+        prod[f"attn_combine_M{M}_pos{pos}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1)}
+        del parts
+    res["producers"] = prod
+
     # decode step capture: 20 layers' linear sequences in one HIP graph
     # (webyiq_amd/layer.py: qkv, o, gate_up, down with their quantisers), the
     # layers sharing one residual stream
     from webyiq_amd.layer import DecodeLayer
     H, Q, KV, F, L = 2048, 2048, 512, 6144, 20
     step = {}
-    for M, fuse in ((1, True), (2, True), (1, False)):
+    for M, fuse, attention in ((1, True, "combine"), (2, True, "combine"), (1, True, "copy"),
+                               (1, False, "copy")):
         x = torch.zeros((M, H), dtype=torch.float32, device="cuda")
         layers = []
         for _ in range(L):
@@ -383,7 +420,8 @@ def bench_configs(torch, lib, ops):
                 w[name] = ops.Q4Tensor(q, sc, c, G)
             w["attn_norm"] = torch.ones(H, dtype=torch.float32, device="cuda")
             w["mlp_norm"] = torch.ones(H, dtype=torch.float32, device="cuda")
-            layers.append(DecodeLayer(w, M, hidden=H, q_dim=Q, kv_dim=KV, ffn=F, G=G, fused=fuse, x=x))
+            layers.append(DecodeLayer(w, M, hidden=H, q_dim=Q, kv_dim=KV, ffn=F, G=G, fused=fuse, x=x,
+                                      attention=attention))
         x0 = torch.randn((M, H), dtype=torch.float32, device="cuda")
 
         class Step:  # the graph_time launch protocol: one callable per captured unit
@@ -394,9 +432,9 @@ def bench_configs(torch, lib, ops):
         graph_time(torch, [Step()], 2)
         t = graph_time(torch, [Step()], 10)
         nbw = sum(lay.weight_bytes() for lay in layers)
-        step[f"M{M}" + ("" if fuse else "_unfused")] = {
-            "us_per_layer": round(t / L * 1e6, 3), "layers": L, "launches_per_layer": 5 if fuse else 9,
-            "weight_GBps": round(nbw / t / 1e9, 1)}
+        key = f"M{M}" + ("" if attention == "combine" else "_copy_attn") + ("" if fuse else "_unfused")
+        step[key] = {"us_per_layer": round(t / L * 1e6, 3), "layers": L, "launches_per_layer": 5 if fuse else 9,
+                     "attention_stand_in": attention, "weight_GBps": round(nbw / t / 1e9, 1)}
         del layers
     res["decode_step_graph"] = step
     torch.cuda.empty_cache()

@@ -210,7 +210,7 @@ int wq_mtp_in(void* stream, const float* emb, const float* x, const float* norm_
  * attention): the gate of (m, h, i) is gate[m * gate_stride + h * 2D + D + i]
  * and the output is divided by 1 + exp(-gate).  xq i8 [M, H*D],
  * dx f32 [M, H*D/32], xs i32 [M, H*D/32]; D in {64, 128, 256},
- * nch <= 4096, pos + M - 1 < 32 nch; xq 16-byte aligned.
+ * nch <= 8192, pos + M - 1 < 32 nch; xq 16-byte aligned.
  */
 int wq_attn_combine(void* stream, const float* part, int64_t M, int64_t H, int64_t D,
                     int64_t nch, int64_t pos, const float* gate, int64_t gate_stride,

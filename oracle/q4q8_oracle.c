@@ -402,7 +402,8 @@ void or_mtp_in(const float* emb, const float* x, const float* nf, const float* n
  *   mx = max m_c; w_c = expf(m_c - mx)
  *   l: lane j (0..63) accumulates fmaf(w_c, l_c, .) over c = j, j + 64, ...,
  *      then the pairwise tree over the 64 lanes (as rms_scale)
- *   o[i] = (fmaf chain of w_c * part_c[i] over c in order) / l
+ *   o[i] = ((o_0 + o_1) + (o_2 + o_3)) / l with o_w the fmaf chain of
+ *      w_c * part_c[i] over c = w, w + 4, ... in order (four wavefronts)
  *   gated: o[i] = o[i] / (1 + expf(-g[i])), g at gate[m*gs + h*2D + D + i]
  *   per 32 dims: dx = amax / 127, xq = rint(o / dx), xs = sum xq.
  * The device's expf may differ from the host's in the last bit, so codes
@@ -431,9 +432,9 @@ void or_attn_combine(const float* part, int64_t M, int64_t H, int64_t D, int64_t
                     if (!(j & off)) p[j] = p[j] + p[j + off];
             const float l = p[0];
             for (int64_t i = 0; i < D; ++i) {
-                float acc = 0.0f;
-                for (int64_t c = 0; c < n; ++c) acc = fmaf(w[c], hb[c * (D + 2) + i], acc);
-                o[i] = acc / l;
+                float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int64_t c = 0; c < n; ++c) acc[c % 4] = fmaf(w[c], hb[c * (D + 2) + i], acc[c % 4]);
+                o[i] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) / l;
                 if (gate) o[i] = o[i] / (1.0f + expf(-gate[m * gs + h * 2 * D + D + i]));
             }
             for (int64_t g = 0; g < D / 32; ++g) {

@@ -154,7 +154,7 @@ def test_attn_combine_argument_errors():
     assert combine(part=None) == _lib.WQ_EINVAL and "part is NULL" in err()
     assert combine(D=96) == _lib.WQ_ESHAPE and "head dim" in err()
     assert combine(M=0) == _lib.WQ_ESHAPE and combine(H=0) == _lib.WQ_ESHAPE
-    assert combine(nch=4097) == _lib.WQ_ESHAPE and "chunks" in err()
+    assert combine(nch=8193) == _lib.WQ_ESHAPE and "chunks" in err()
     assert combine(nch=4, pos=128) == _lib.WQ_ESHAPE and "context" in err()
     assert combine(nch=4, pos=126, M=3) == _lib.WQ_ESHAPE     # token 2 at position 128
     assert combine(pos=-1) == _lib.WQ_ESHAPE

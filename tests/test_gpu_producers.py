@@ -101,3 +101,56 @@ def test_attn_combine_feeds_the_o_projection():
     a = ops.attn_combine(dev(part), pos, G=G)
     y = ops.gemv(ops.Q4Tensor(dev(wq.view(np.int32)), dev(ws.view(np.int32)), H * D, G), a)
     assert np.array_equal(host(y), y_r)
+
+
+def test_decode_layer_with_attention_combine():
+    """The layer's decode order with the chunk merge (graph.rs:289-291):
+    combine -> o (plain GEMV on per-32 activations) equals the oracle's
+    combine and linear bit for bit, and graph replays reproduce the eager run."""
+    from webyiq_amd.layer import DecodeLayer
+    note("decode layer attention=combine")
+    M, H, Q, KV, F, G, D, pos = 2, 1024, 1024, 256, 2048, 128, 128, 300
+    rng = np.random.default_rng(31)
+    shapes = {"qkv": (Q + 2 * KV, H), "o": (H, Q), "gate_up": (2 * F, H), "down": (H, F)}
+    host_w = {n: ref.make_weight(rng, r, c, G) for n, (r, c) in shapes.items()}
+    w = ops.Weights({n: ops.Q4Tensor.from_numpy(q, s, shapes[n][1], G) for n, (q, s) in host_w.items()})
+    w["attn_norm"] = dev(rng.normal(1, 0.1, H).astype(np.float32))
+    w["mlp_norm"] = dev(rng.normal(1, 0.1, H).astype(np.float32))
+    x0 = dev(ref.make_activations(rng, M, H))
+    layer = DecodeLayer(w, M, hidden=H, q_dim=Q, kv_dim=KV, ffn=F, G=G, attention="combine", head_dim=D,
+                        pos=pos, max_ctx=1024)
+    part = make_part(rng, M, Q // D, D, 1024 // 32, pos, equal_max=True)
+    layer.part.copy_(dev(part))
+
+    # combine -> o alone against the oracle
+    xq, dx, xs = orc.attn_combine(part, pos)
+    a = ops.attn_combine(layer.part, pos)
+    for got, exp in zip((a.xq, a.dx, a.xs), (xq, dx, xs)):
+        assert np.array_equal(host(got), exp)
+    y0 = host(x0).copy()
+    y_want = orc.linear(*host_w["o"], Q, G, xq, dx, xs, mode=1, y=y0.copy(), GA=32)
+    y = x0.clone()
+    ops.gemv(w.w("o"), a, mode=ops.MODE_ACCUMULATE, y=y)
+    assert np.array_equal(host(y).view(np.uint32), y_want.view(np.uint32))
+
+    layer.x.copy_(x0)
+    layer.run()
+    want = host(layer.x).copy()
+    assert np.all(np.isfinite(want))
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        layer.x.copy_(x0)
+        layer.run()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        layer.x.copy_(x0)
+        layer.run()
+    for i in range(3):
+        g.replay()
+        got = host(layer.x)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"replay {i}"
+        layer.x.add_(1.0)  # eager work between replays
+        torch.cuda.synchronize()

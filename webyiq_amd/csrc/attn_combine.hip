@@ -12,12 +12,13 @@
 //   per 32 dims: dx = amax / 127, xq = rint(o / dx) (IEEE quotient, as the
 //   activation quantiser), xs = sum of xq.
 //
-// One wavefront per (token, head), four per workgroup, no barriers: lane l
-// owns dims DPL l .. DPL l + DPL - 1 (DPL = D / 64).  Order of the sums, which
-// the CPU oracle restates: l -- lane l accumulates fmaf(w_c, l_c, .) over
-// chunks c = l, l + 64, ... in order, then the lanes' pairwise tree
-// (wave_sum_tree); o -- one fmaf chain per dim over the chunks in order.
-// The chunk weights go through LDS (one word per chunk and wave).
+// One workgroup of four wavefronts per (token, head); lane l owns dims
+// DPL l .. DPL l + DPL - 1 (DPL = D / 64).  Order of the sums, which the CPU
+// oracle restates: l -- lane l accumulates fmaf(w_c, l_c, .) over chunks
+// c = l, l + 64, ... in order, then the lanes' pairwise tree
+// (wave_sum_tree); o -- wave w runs one fmaf chain per dim over the chunks
+// c = w, w + 4, w + 8, ... in order, and the four chains are added as
+// (o_0 + o_1) + (o_2 + o_3).  The chunk weights go through LDS.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -56,60 +57,69 @@ __global__ __launch_bounds__(64 * kCombineWaves) void attn_combine_kernel(AttnCo
     pin_arg(a.gate); pin_arg(a.gate_stride); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
     constexpr int D = 64 * DPL;
     constexpr int LPG = 32 / DPL;  // lanes per 32-dim group
-    extern __shared__ float wsh[];  // [waves][nch] chunk weights
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t item = (int64_t)blockIdx.x * kCombineWaves + wave;  // m * H + h
-    if (item >= a.M * a.H) return;  // whole wavefronts; the kernel has no barrier
+    constexpr int UNROLL = 8;      // chunks in flight per wavefront
+    extern __shared__ float sh[];  // chunk weights [nch] | chains of waves 1..3 [3][D]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t item = blockIdx.x;  // m * H + h
     const int64_t m = item / a.H, h = item - m * a.H;
     const int nch = (int)a.nch;
     const int n = (int)((a.pos + m + kChunk) / kChunk);  // <= nch (checked on the host)
     const float* hb = a.part + item * (int64_t)nch * (D + 2);
-    float* w = wsh + wave * nch;
+    float* w = sh;
+    float* chains = sh + nch;
 
-    // chunk maxima, lane-parallel (attn_combine.wgsl:39-42)
+    // chunk maxima (attn_combine.wgsl:39-42), in every wavefront
     float ml = -3.0e38f;
     for (int c = lane; c < n; c += 64) ml = fmaxf(ml, hb[(int64_t)c * (D + 2) + D]);
     const float mx = wave_max(ml);
-    // weights and their sum (:43-47)
-    float ll = 0.0f;
-    for (int c = lane; c < n; c += 64) {
-        const float* cb = hb + (int64_t)c * (D + 2);
-        const float wc = expf(cb[D] - mx);
-        w[c] = wc;
-        ll = fmaf(wc, cb[D + 1], ll);
-    }
-    const float l = wave_sum_tree(ll);
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // chunk weights (:46), once per workgroup
+    for (int c = tid; c < n; c += 64 * kCombineWaves) w[c] = expf(hb[(int64_t)c * (D + 2) + D] - mx);
+    __syncthreads();
 
-    // weighted sums of the chunk outputs, one chain per dim (:48)
+    // wave w's chains over chunks w, w + 4, ... (:48)
     float acc[DPL];
 #pragma unroll
     for (int k = 0; k < DPL; ++k) acc[k] = 0.0f;
     const float* pl = hb + DPL * lane;
-    int c = 0;
-    for (; c + 4 <= n; c += 4) {
-        float p[4][DPL], wc[4];
+    int c = wave;
+    for (; c + kCombineWaves * (UNROLL - 1) < n; c += kCombineWaves * UNROLL) {
+        float p[UNROLL][DPL], wc[UNROLL];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            wc[q] = w[c + q];
+        for (int q = 0; q < UNROLL; ++q) {
+            const int cq = c + kCombineWaves * q;
+            wc[q] = w[cq];
 #pragma unroll
-            for (int k = 0; k < DPL; ++k) p[q][k] = pl[(int64_t)(c + q) * (D + 2) + k];
+            for (int k = 0; k < DPL; ++k) p[q][k] = pl[(int64_t)cq * (D + 2) + k];
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+        for (int q = 0; q < UNROLL; ++q)
 #pragma unroll
             for (int k = 0; k < DPL; ++k) acc[k] = fmaf(wc[q], p[q][k], acc[k]);
     }
-    for (; c < n; ++c) {
+    for (; c < n; c += kCombineWaves) {
         const float wc = w[c];
 #pragma unroll
         for (int k = 0; k < DPL; ++k) acc[k] = fmaf(wc, pl[(int64_t)c * (D + 2) + k], acc[k]);
     }
+    if (wave > 0) {
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) chains[(wave - 1) * D + DPL * lane + k] = acc[k];
+    }
+    // weight sum (:47), lane-parallel then the lane tree
+    float ll = 0.0f;
+    if (wave == 0)
+        for (int cc = lane; cc < n; cc += 64) ll = fmaf(w[cc], hb[(int64_t)cc * (D + 2) + D + 1], ll);
+    __syncthreads();
+    if (wave > 0) return;  // no barrier follows
+    const float l = wave_sum_tree(ll);
+
     float o[DPL];
 #pragma unroll
-    for (int k = 0; k < DPL; ++k) o[k] = acc[k] / l;  // :50
+    for (int k = 0; k < DPL; ++k) {
+        const int i = DPL * lane + k;
+        const float s = (acc[k] + chains[i]) + (chains[D + i] + chains[2 * D + i]);
+        o[k] = s / l;  // :50
+    }
     if (a.gate) {  // :51-54, gate rows [head: q (D) | gate (D)]
         const float* g = a.gate + m * a.gate_stride + h * 2 * D + D + DPL * lane;
 #pragma unroll
@@ -146,8 +156,8 @@ __global__ __launch_bounds__(64 * kCombineWaves) void attn_combine_kernel(AttnCo
 }  // namespace
 
 hipError_t launch_attn_combine(const AttnCombineArgs& a, hipStream_t s) {
-    dim3 grid((unsigned)((a.M * a.H + kCombineWaves - 1) / kCombineWaves)), block(64 * kCombineWaves);
-    const size_t lds = (size_t)kCombineWaves * a.nch * sizeof(float);
+    dim3 grid((unsigned)(a.M * a.H)), block(64 * kCombineWaves);
+    const size_t lds = ((size_t)a.nch + 3 * (size_t)a.D) * sizeof(float);
     switch (a.D) {
         case 64: hipLaunchKernelGGL((attn_combine_kernel<1>), grid, block, lds, s, a); break;
         case 128: hipLaunchKernelGGL((attn_combine_kernel<2>), grid, block, lds, s, a); break;

@@ -67,8 +67,8 @@ struct MtpInArgs {
 
 // Flash-decoding merge of per-chunk attention partials, emitted as per-32
 // int8 groups for the o projection (nch <= kCombineMaxChunks: the chunk
-// weights of four wavefronts fit 64 KiB of LDS).
-constexpr int kCombineMaxChunks = 4096;
+// weights and three partial chains fit 64 KiB of LDS).
+constexpr int kCombineMaxChunks = 8192;
 struct AttnCombineArgs {
     const float* part;    // [M, H, nch, D + 2]: chunk output sums, chunk max, chunk sum
     int64_t M, H, D, nch;

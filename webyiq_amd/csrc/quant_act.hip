@@ -263,15 +263,25 @@ __global__ __launch_bounds__(kQuantThreads) void mtp_in_kernel(MtpInArgs a) {
     const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
     auto chunk = [&](int j, int u) { return kPassChunks * j + 64 * u + lane; };
 
+    // rows of one pass: the input and both norm weights in registers, all
+    // loaded up front; longer rows: the input cached for up to 3 passes, the
+    // weights read (L2 hits) where they are used
     constexpr int NC = JC > 0 ? JC : 1;
-    float4 xc[NC][8];
+    constexpr bool WREG = JC == 1;
+    const float* w0 = hidden ? a.norm_f : a.norm_e;
+    float4 xc[NC][8], wc0[8], wc1[8];
     if (JC > 0) {
 #pragma unroll
         for (int j = 0; j < NC; ++j)
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int c = chunk(j, u);
-                xc[j][u] = j < J && c < nchunk ? src[c] : zero4;
+                const bool ok = j < J && c < nchunk;
+                xc[j][u] = ok ? src[c] : zero4;
+                if (WREG && j == 0) {
+                    wc0[u] = ok ? reinterpret_cast<const float4*>(w0)[c] : zero4;
+                    wc1[u] = ok && hidden ? reinterpret_cast<const float4*>(a.norm_h)[c] : zero4;
+                }
             }
     }
     auto raw = [&](int j, int u) -> float4 {
@@ -279,9 +289,11 @@ __global__ __launch_bounds__(kQuantThreads) void mtp_in_kernel(MtpInArgs a) {
         const int c = chunk(j, u);
         return c < nchunk ? src[c] : zero4;
     };
-    auto weight = [&](const float* w, int j, int u) -> float4 {
+    // norm weight 0 (norm_e or norm_f) or 1 (norm_h) of chunk (j, u)
+    auto weight = [&](int which, int j, int u) -> float4 {
+        if (WREG) return which ? wc1[u] : wc0[u];
         const int c = chunk(j, u);
-        return c < nchunk ? reinterpret_cast<const float4*>(w)[c] : zero4;
+        return c < nchunk ? reinterpret_cast<const float4*>(which ? a.norm_h : w0)[c] : zero4;
     };
     auto scale = [](float4 v, float r, float4 w) {  // mtp_in.wgsl:56,65,70: v *= r * w
         v.x = v.x * (r * w.x);
@@ -313,11 +325,10 @@ __global__ __launch_bounds__(kQuantThreads) void mtp_in_kernel(MtpInArgs a) {
     };
 
     const float r0 = inv_rms(raw);
-    const float* w0 = hidden ? a.norm_f : a.norm_e;
-    auto v0 = [&](int j, int u) { return scale(raw(j, u), r0, weight(w0, j, u)); };
+    auto v0 = [&](int j, int u) { return scale(raw(j, u), r0, weight(0, j, u)); };
     float r1 = 0.0f;
     if (hidden) r1 = inv_rms(v0);
-    auto out = [&](int j, int u) { return hidden ? scale(v0(j, u), r1, weight(a.norm_h, j, u)) : v0(j, u); };
+    auto out = [&](int j, int u) { return hidden ? scale(v0(j, u), r1, weight(1, j, u)) : v0(j, u); };
 
     QuantArgs q{};
     q.K = a.K;
