@@ -87,11 +87,12 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     const int64_t r0 = (int64_t)blockIdx.x * RB;
 
     // LDS: group sums [MT][NH][RB][NEP] i32 | weight (s, m) [NH][RB][NG] f32x2 |
-    //      activation sums [MT][NE] f32 | activation scales [MT][NDX] f32
+    //      activation sums [MT][NE] f32 | activation scales [MT][NDX] f32,
+    //      each part 16-byte aligned (the epilogue reads them 16 bytes at a time)
     int32_t* acc_lds = reinterpret_cast<int32_t*>(smem);
     float2* sm_lds = reinterpret_cast<float2*>(acc_lds + (size_t)MT * NH * RB * NEP);
-    float* xs_lds = reinterpret_cast<float*>(sm_lds + (size_t)NH * RB * NGS);
-    float* dx_lds = xs_lds + (size_t)MT * NE;
+    float* xs_lds = lds_align<16, float>(smem, sm_lds + (size_t)NH * RB * NGS);
+    float* dx_lds = lds_align<16, float>(smem, xs_lds + (size_t)MT * NE);
     // fused quantiser scratch (QIN kernels have no argmax keys)
     static_assert(!(QIN && ARGMAX), "no fused quantiser in the lm_head kernel");
     float* qin_lds = lds_align<16, float>(smem, dx_lds + (size_t)MT * NDX);
@@ -354,12 +355,24 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
             }
             return acc * dr[0];
         } else {
-#pragma unroll 8
-            for (int ee = 0; ee < NE; ++ee) {
-                float2 w = sr[(ee * 32) / G];
-                float d = dr[ee];
-                acc = fmaf(w.x * d, (float)ar[ee], acc);
-                acc = fmaf(w.y * d, xsr[ee], acc);
+            // per-32 activation scales: the same chain, its operands read four
+            // groups at a time (NE = K/32 is a multiple of 4)
+#pragma unroll 2
+            for (int ee = 0; ee < NE; ee += 4) {
+                const int4 a4 = *reinterpret_cast<const int4*>(ar + ee);
+                const float4 x4 = *reinterpret_cast<const float4*>(xsr + ee);
+                const float4 d4 = *reinterpret_cast<const float4*>(dr + ee);
+                float2 w[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) w[q] = sr[((ee + q) * 32) / G];
+                acc = fmaf(w[0].x * d4.x, (float)a4.x, acc);
+                acc = fmaf(w[0].y * d4.x, x4.x, acc);
+                acc = fmaf(w[1].x * d4.y, (float)a4.y, acc);
+                acc = fmaf(w[1].y * d4.y, x4.y, acc);
+                acc = fmaf(w[2].x * d4.z, (float)a4.z, acc);
+                acc = fmaf(w[2].y * d4.z, x4.z, acc);
+                acc = fmaf(w[3].x * d4.w, (float)a4.w, acc);
+                acc = fmaf(w[3].y * d4.w, x4.w, acc);
             }
             return acc;
         }
@@ -495,6 +508,7 @@ Plan make_plan(const LinearArgs& a, bool argmax, bool qin = false) {
                    (size_t)p.MT * p.NE * 4 + (size_t)p.MT * (pt ? 1 : a.K / 32) * 4;
         if (argmax) b += 16 + (size_t)p.MT * rb * 8;
         if (qin) b += (size_t)p.MT * (16 * 4 + 8 * 64 * 4 + a.K) + 32;
+        b += 32;  // 16-byte alignment of the activation sums and scales
         return b;
     };
     // registers: weights in flight (4 per row half) + activations (8 per token)
