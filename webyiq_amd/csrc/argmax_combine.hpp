@@ -9,6 +9,30 @@
 
 namespace wq {
 
+// The workgroup's best key per token from its keys [MT][RB] in LDS, for
+// thread t < min(MT, M) (0 elsewhere).  32 lanes per token each fold every
+// 32nd key, then an xor-shuffle maximum over the 32 (the workgroup has at
+// least 256 threads, so MT <= 8 tokens fit); the results meet in LDS.
+template <int MT>
+__device__ __forceinline__ unsigned long long block_best(const unsigned long long* keys, int RB, int M) {
+    static_assert(MT * 32 <= 256, "32 lanes per token");
+    __shared__ unsigned long long tok_best[MT];
+    const int tid = threadIdx.x;
+    const int t = tid >> 5, j = tid & 31;
+    if (t < MT) {
+        unsigned long long v = 0;
+        for (int rl = j; rl < RB; rl += 32) v = keys[t * RB + rl] > v ? keys[t * RB + rl] : v;
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) {
+            const unsigned long long u = __shfl_xor(v, o, 32);
+            v = u > v ? u : v;
+        }
+        if (j == 0) tok_best[t] = v;
+    }
+    __syncthreads();
+    return tid < MT && tid < M ? tok_best[tid] : 0ull;
+}
+
 // Every workgroup calls this once with its best key for token tid in
 // threads tid < M (0 elsewhere).  No memory fence is used (a device-scope
 // release would write back the XCD's L2): keys and tickets live in

@@ -255,9 +255,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
         keys[o] = key;
     }
     __syncthreads();
-    unsigned long long best = 0;
-    if (tid < MT && tid < a.M)
-        for (int rl = 0; rl < RB; ++rl) best = keys[tid * RB + rl] > best ? keys[tid * RB + rl] : best;
+    const unsigned long long best = block_best<MT>(keys, RB, (int)a.M);
     argmax_combine<MT>(p.am, (int)a.M, p.nblocks, best);
 }
 
