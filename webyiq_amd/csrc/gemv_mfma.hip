@@ -69,6 +69,11 @@ template <int MT, int MODE, int RBW, bool ARGMAX>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
     constexpr int NH = MODE == 2 ? 2 : 1;  // gate (+ up) row halves
     constexpr int RB = 16 * RBW;           // rows per workgroup
+    // RBW == 4: each wave owns all groups of its 16 rows (K <= 2048), so the
+    // group sums stay in the MFMA result registers and each lane runs the
+    // fp32 chains of its row and tokens there; otherwise the K split meets
+    // through LDS
+    constexpr bool REG = RBW == kWaves;
     extern __shared__ __align__(16) unsigned char smem[];
     const LinearArgs& a = p.a;
     pin_arg(a.wq); pin_arg(a.ws); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs); pin_arg(a.y);
@@ -90,11 +95,11 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
     const int64_t r0 = (int64_t)blockIdx.x * RB;
     const int c = lane & 15, q = lane >> 4;
 
-    // LDS: group sums [MT][NH][RB][NGP] i32 | (s, m) [NH][RB][NGP] f32x2 |
+    // LDS: group sums [MT][NH][RB][NGP] i32 (not with REG) | (s, m) [NH][RB][NGP] f32x2 |
     //      activation group sums [MT * NG, 64-rounded] i32 | scales [64] f32 |
-    //      int8 activations [MT][K]
+    //      int8 activations [MT][K] | per-wave best keys [4][MT] (REG)
     int32_t* acc_lds = reinterpret_cast<int32_t*>(smem);
-    float2* sm_lds = reinterpret_cast<float2*>(acc_lds + (size_t)MT * NH * RB * NGP);
+    float2* sm_lds = reinterpret_cast<float2*>(acc_lds + (REG ? 0 : (size_t)MT * NH * RB * NGP));
     int32_t* xs_lds = reinterpret_cast<int32_t*>(sm_lds + (size_t)NH * RB * NGP);
     float* dx_lds = reinterpret_cast<float*>(xs_lds + ((MT * NG + 63) & ~63));
     unsigned char* xq_lds = reinterpret_cast<unsigned char*>(dx_lds + 64);
@@ -139,6 +144,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
     // 3. per group: two MFMAs (codes 32 q .. +15, then +16 .. +31 of the group)
     const int m = c < MT ? c : MT - 1;  // token of this lane's activation operand
     const unsigned char* xr = xq_lds + m * K + 16 * 2 * q;
+    v4i dres[NH][REG ? kMaxGpw : 1];  // REG: group sums of (row c, tokens 4 q ..)
 #pragma unroll
     for (int i = 0; i < kMaxGpw; ++i) {
         if (i >= ng) continue;
@@ -154,10 +160,14 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
             v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, v4i{0, 0, 0, 0}, 0, 0, 0);
             d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, d, 0, 0, 0);
             // lane (row c, quarter q) holds tokens 4 q .. 4 q + 3
+            if constexpr (REG) {
+                dres[h][i] = d;
+            } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int t = 4 * q + j;
-                if (t < MT) acc_lds[((t * NH + h) * RB + 16 * blk + c) * NGP + g] = d[j];
+                for (int j = 0; j < 4; ++j) {
+                    const int t = 4 * q + j;
+                    if (t < MT) acc_lds[((t * NH + h) * RB + 16 * blk + c) * NGP + g] = d[j];
+                }
             }
         }
     }
@@ -171,6 +181,93 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
         }
     }
     __syncthreads();
+
+    if constexpr (REG) {
+        // 4'. fp32 chains in registers: lane (row c, quarter q) folds tokens
+        //     4 q .. 4 q + 3 of its row over the groups in order, the same
+        //     operations as the LDS chain below
+        const int64_t rr = r0 + 16 * blk + c;  // this lane's row (unclamped)
+        float acc[NH][4];
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[h][j] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMaxGpw; ++i) {
+            if (i >= ng) continue;  // ng == NG here
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const float2 w = sm_lds[(h * RB + 16 * blk + c) * NGP + i];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
+                    acc[h][j] = fmaf(w.x, (float)dres[h][i][j], acc[h][j]);
+                    acc[h][j] = fmaf(w.y, (float)xs_lds[t * NG + i], acc[h][j]);
+                }
+            }
+        }
+        float v[NH][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
+#pragma unroll
+            for (int h = 0; h < NH; ++h) v[h][j] = acc[h][j] * dx_lds[t];
+        }
+        if (a.acc_dump) {  // test hook: the group sums the chains folded
+            const int rows_total = NH * (int)N;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int t = 4 * q + j;
+                if (t < a.M && rr < N)
+#pragma unroll
+                    for (int h = 0; h < NH; ++h)
+#pragma unroll
+                        for (int i = 0; i < kMaxGpw; ++i)  // constant indices: registers
+                            if (i < ng) a.acc_dump[((int64_t)t * rows_total + h * N + rr) * NG + i] = dres[h][i][j];
+            }
+        }
+        if (!ARGMAX) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int t = 4 * q + j;
+                if (t >= a.M || rr >= N) continue;
+                float* yo = a.y + (int64_t)t * N + rr;
+                if (MODE == 0) {
+                    *yo = v[0][j];
+                } else if (MODE == 1) {
+                    *yo = *yo + v[0][j];
+                } else {
+                    *yo = silu_mul(v[0][j], v[NH - 1][j]);
+                }
+            }
+            return;
+        }
+        // fused greedy argmax: keys of this lane's (token, row), the maximum
+        // over the wave's 16 rows by shuffles, over the 4 waves through LDS
+        unsigned long long* wbest = reinterpret_cast<unsigned long long*>(xq_lds + (size_t)MT * K);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = 4 * q + j;
+            unsigned long long key = 0;
+            if (t < a.M && rr < N) {
+                if (a.y) a.y[(int64_t)t * N + rr] = v[0][j];
+                if (v[0][j] > -3.0e38f) key = argmax_key(v[0][j], (uint32_t)rr);
+            }
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) {
+                const unsigned long long u = __shfl_xor(key, o, 16);
+                key = u > key ? u : key;
+            }
+            if (c == 0 && t < MT) wbest[wave * MT + t] = key;
+        }
+        __syncthreads();
+        unsigned long long best = 0;
+        if (tid < MT && tid < a.M)
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) best = wbest[w * MT + tid] > best ? wbest[w * MT + tid] : best;
+        argmax_combine<MT>(p.am, (int)a.M, p.nblocks, best);
+        return;
+    }
 
     if (a.acc_dump) {  // test hook: the group sums exactly as the epilogue reads them
         const int rows_total = NH * (int)N;
@@ -295,8 +392,10 @@ hipError_t launch_gemv_mfma(const LinearArgs& a, const ArgmaxArgs* am, hipStream
     const int rb = 16 * rbw, nh = a.mode == 2 ? 2 : 1, mt = 8;
     const unsigned grid = (unsigned)((a.N + rb - 1) / rb);
     gp.nblocks = (int)grid;
-    const size_t lds = (size_t)mt * nh * rb * gp.NGP * 4 + (size_t)nh * rb * gp.NGP * 8 +
-                       (size_t)((mt * NG + 63) & ~63) * 4 + 64 * 4 + (size_t)mt * a.K;
+    // (rbw == 4: no group-sum buffer, the per-wave best keys instead)
+    const size_t lds = (rbw == kWaves ? (size_t)kWaves * mt * 8 : (size_t)mt * nh * rb * gp.NGP * 4) +
+                       (size_t)nh * rb * gp.NGP * 8 + (size_t)((mt * NG + 63) & ~63) * 4 + 64 * 4 +
+                       (size_t)mt * a.K;
     if (am) return launch_rbw<8, 0, true>(gp, rbw, lds, grid, s);
     switch (a.mode) {
         case 0: return launch_rbw<8, 0, false>(gp, rbw, lds, grid, s);
