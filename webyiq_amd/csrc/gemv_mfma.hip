@@ -13,10 +13,12 @@
 // 16 codes per MFMA), the same code subset for both operands, so each
 // result is an exact int32 group sum.  Weight chunks (16 bytes per lane and
 // group) are all issued before the first is used; the int8 activations are
-// staged in LDS once per workgroup.  The group sums go to LDS and the fp32
-// epilogue is the dot4 kernel's -- one chain per (token, row) over the groups
-// in index order, acc = fma(s, A, acc); acc = fma(m, X, acc); y = acc * dx
-// -- so outputs are bit-identical to it and to the oracle.
+// staged in LDS once per workgroup.  The fp32 epilogue is the dot4 kernel's
+// -- one chain per (token, row) over the groups in index order,
+// acc = fma(s, A, acc); acc = fma(m, X, acc); y = acc * dx -- so outputs are
+// bit-identical to it and to the oracle.  For K <= 2048 (gemv_mfma_rows_kernel)
+// a wave owns every group of its rows and the chains run in the MFMA result
+// registers; for longer rows the K split meets through LDS.
 #include "argmax_combine.hpp"
 #include "common.hpp"
 #include "launch.hpp"
@@ -28,6 +30,11 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kMaxGpw = 16;  // groups per wave
+// waves per workgroup of the K <= 2048 register-chain kernel
+#ifndef WQ_MFMA_ROWS_WAVES
+#define WQ_MFMA_ROWS_WAVES 4
+#endif
+constexpr int kRowsWaves = WQ_MFMA_ROWS_WAVES;
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -69,11 +76,6 @@ template <int MT, int MODE, int RBW, bool ARGMAX>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
     constexpr int NH = MODE == 2 ? 2 : 1;  // gate (+ up) row halves
     constexpr int RB = 16 * RBW;           // rows per workgroup
-    // RBW == 4: each wave owns all groups of its 16 rows (K <= 2048), so the
-    // group sums stay in the MFMA result registers and each lane runs the
-    // fp32 chains of its row and tokens there; otherwise the K split meets
-    // through LDS
-    constexpr bool REG = RBW == kWaves;
     extern __shared__ __align__(16) unsigned char smem[];
     const LinearArgs& a = p.a;
     pin_arg(a.wq); pin_arg(a.ws); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs); pin_arg(a.y);
@@ -95,11 +97,11 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
     const int64_t r0 = (int64_t)blockIdx.x * RB;
     const int c = lane & 15, q = lane >> 4;
 
-    // LDS: group sums [MT][NH][RB][NGP] i32 (not with REG) | (s, m) [NH][RB][NGP] f32x2 |
+    // LDS: group sums [MT][NH][RB][NGP] i32 | (s, m) [NH][RB][NGP] f32x2 |
     //      activation group sums [MT * NG, 64-rounded] i32 | scales [64] f32 |
-    //      int8 activations [MT][K] | per-wave best keys [4][MT] (REG)
+    //      int8 activations [MT][K]
     int32_t* acc_lds = reinterpret_cast<int32_t*>(smem);
-    float2* sm_lds = reinterpret_cast<float2*>(acc_lds + (REG ? 0 : (size_t)MT * NH * RB * NGP));
+    float2* sm_lds = reinterpret_cast<float2*>(acc_lds + (size_t)MT * NH * RB * NGP);
     int32_t* xs_lds = reinterpret_cast<int32_t*>(sm_lds + (size_t)NH * RB * NGP);
     float* dx_lds = reinterpret_cast<float*>(xs_lds + ((MT * NG + 63) & ~63));
     unsigned char* xq_lds = reinterpret_cast<unsigned char*>(dx_lds + 64);
@@ -144,7 +146,6 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
     // 3. per group: two MFMAs (codes 32 q .. +15, then +16 .. +31 of the group)
     const int m = c < MT ? c : MT - 1;  // token of this lane's activation operand
     const unsigned char* xr = xq_lds + m * K + 16 * 2 * q;
-    v4i dres[NH][REG ? kMaxGpw : 1];  // REG: group sums of (row c, tokens 4 q ..)
 #pragma unroll
     for (int i = 0; i < kMaxGpw; ++i) {
         if (i >= ng) continue;
@@ -160,14 +161,10 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
             v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, v4i{0, 0, 0, 0}, 0, 0, 0);
             d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, d, 0, 0, 0);
             // lane (row c, quarter q) holds tokens 4 q .. 4 q + 3
-            if constexpr (REG) {
-                dres[h][i] = d;
-            } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int t = 4 * q + j;
-                    if (t < MT) acc_lds[((t * NH + h) * RB + 16 * blk + c) * NGP + g] = d[j];
-                }
+            for (int j = 0; j < 4; ++j) {
+                const int t = 4 * q + j;
+                if (t < MT) acc_lds[((t * NH + h) * RB + 16 * blk + c) * NGP + g] = d[j];
             }
         }
     }
@@ -181,93 +178,6 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
         }
     }
     __syncthreads();
-
-    if constexpr (REG) {
-        // 4'. fp32 chains in registers: lane (row c, quarter q) folds tokens
-        //     4 q .. 4 q + 3 of its row over the groups in order, the same
-        //     operations as the LDS chain below
-        const int64_t rr = r0 + 16 * blk + c;  // this lane's row (unclamped)
-        float acc[NH][4];
-#pragma unroll
-        for (int h = 0; h < NH; ++h)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[h][j] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kMaxGpw; ++i) {
-            if (i >= ng) continue;  // ng == NG here
-#pragma unroll
-            for (int h = 0; h < NH; ++h) {
-                const float2 w = sm_lds[(h * RB + 16 * blk + c) * NGP + i];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
-                    acc[h][j] = fmaf(w.x, (float)dres[h][i][j], acc[h][j]);
-                    acc[h][j] = fmaf(w.y, (float)xs_lds[t * NG + i], acc[h][j]);
-                }
-            }
-        }
-        float v[NH][4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
-#pragma unroll
-            for (int h = 0; h < NH; ++h) v[h][j] = acc[h][j] * dx_lds[t];
-        }
-        if (a.acc_dump) {  // test hook: the group sums the chains folded
-            const int rows_total = NH * (int)N;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int t = 4 * q + j;
-                if (t < a.M && rr < N)
-#pragma unroll
-                    for (int h = 0; h < NH; ++h)
-#pragma unroll
-                        for (int i = 0; i < kMaxGpw; ++i)  // constant indices: registers
-                            if (i < ng) a.acc_dump[((int64_t)t * rows_total + h * N + rr) * NG + i] = dres[h][i][j];
-            }
-        }
-        if (!ARGMAX) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int t = 4 * q + j;
-                if (t >= a.M || rr >= N) continue;
-                float* yo = a.y + (int64_t)t * N + rr;
-                if (MODE == 0) {
-                    *yo = v[0][j];
-                } else if (MODE == 1) {
-                    *yo = *yo + v[0][j];
-                } else {
-                    *yo = silu_mul(v[0][j], v[NH - 1][j]);
-                }
-            }
-            return;
-        }
-        // fused greedy argmax: keys of this lane's (token, row), the maximum
-        // over the wave's 16 rows by shuffles, over the 4 waves through LDS
-        unsigned long long* wbest = reinterpret_cast<unsigned long long*>(xq_lds + (size_t)MT * K);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int t = 4 * q + j;
-            unsigned long long key = 0;
-            if (t < a.M && rr < N) {
-                if (a.y) a.y[(int64_t)t * N + rr] = v[0][j];
-                if (v[0][j] > -3.0e38f) key = argmax_key(v[0][j], (uint32_t)rr);
-            }
-#pragma unroll
-            for (int o = 8; o > 0; o >>= 1) {
-                const unsigned long long u = __shfl_xor(key, o, 16);
-                key = u > key ? u : key;
-            }
-            if (c == 0 && t < MT) wbest[wave * MT + t] = key;
-        }
-        __syncthreads();
-        unsigned long long best = 0;
-        if (tid < MT && tid < a.M)
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) best = wbest[w * MT + tid] > best ? wbest[w * MT + tid] : best;
-        argmax_combine<MT>(p.am, (int)a.M, p.nblocks, best);
-        return;
-    }
 
     if (a.acc_dump) {  // test hook: the group sums exactly as the epilogue reads them
         const int rows_total = NH * (int)N;
@@ -356,11 +266,192 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
     argmax_combine<MT>(p.am, (int)a.M, p.nblocks, best);
 }
 
+// K <= 2048 (at most 16 groups): every wave owns all groups of a 16-row
+// block, the group sums stay in the MFMA result registers and each lane runs
+// the fp32 chains of its row and four tokens there, in the LDS chain's order
+// (no group-sum buffer: ~27 KB of LDS, five workgroups per CU).  Measured
+// against 2 and 8 waves per workgroup, 4 is fastest.
+template <int MT, int MODE, bool ARGMAX>
+__global__ __launch_bounds__(64 * kRowsWaves) void gemv_mfma_rows_kernel(MfmaGemvParams p) {
+    constexpr int NH = MODE == 2 ? 2 : 1;
+    constexpr int RB = 16 * kRowsWaves;  // rows per workgroup: one 16-row block per wave
+    constexpr int NT = 64 * kRowsWaves;  // threads
+    extern __shared__ __align__(16) unsigned char smem[];
+    const LinearArgs& a = p.a;
+    pin_arg(a.wq); pin_arg(a.ws); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs); pin_arg(a.y);
+    pin_arg(a.acc_dump); pin_arg(a.N); pin_arg(a.K); pin_arg(a.M); pin_arg(p.NG); pin_arg(p.NGP);
+    if (ARGMAX) {
+        pin_arg(p.am.ids); pin_arg(p.am.tok_out); pin_arg(p.am.keys); pin_arg(p.am.ticket);
+        pin_arg(p.nblocks);
+    }
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int K = (int)a.K;
+    const int NG = p.NG, NGP = p.NGP;  // NG <= kMaxGpw
+    const int64_t N = a.N;
+    const int c = lane & 15, q = lane >> 4;
+
+    // LDS: (s, m) [NH][RB][NGP] f32x2 | activation group sums [MT * NG, 64-rounded] i32 |
+    //      scales [64] f32 | int8 activations [MT][K] | per-wave best keys [waves][MT]
+    float2* sm_lds = reinterpret_cast<float2*>(smem);
+    int32_t* xs_lds = reinterpret_cast<int32_t*>(sm_lds + (size_t)NH * RB * NGP);
+    float* dx_lds = reinterpret_cast<float*>(xs_lds + ((MT * NG + 63) & ~63));
+    unsigned char* xq_lds = reinterpret_cast<unsigned char*>(dx_lds + 64);
+    unsigned long long* wbest = reinterpret_cast<unsigned long long*>(xq_lds + (size_t)MT * K);
+
+    // the activations, once per workgroup (direct to LDS)
+    const int xchunks = (int)(a.M * K / 16);
+    for (int base = 64 * wave; base < xchunks; base += NT)
+        dma16(a.xq, 16u * (uint32_t)(base + lane < xchunks ? base + lane : 0), xq_lds + 16 * base);
+    const int nxs = (int)a.M * NG;
+    for (int base = 64 * wave; base < nxs; base += NT)
+        dma4(a.xs, 4u * (uint32_t)(base + lane < nxs ? base + lane : 0), xs_lds + base);
+    if (wave == 0) dma4(a.dx, 4u * (uint32_t)(lane < a.M ? lane : 0), dx_lds);
+
+    const int m = c < MT ? c : MT - 1;  // token of this lane's activation operand
+    const unsigned char* xr = xq_lds + m * K + 16 * 2 * q;
+    unsigned long long best[4] = {0, 0, 0, 0};  // keys of tokens 4 q + j (this lane's row)
+
+    {
+        const int64_t rr = (int64_t)blockIdx.x * RB + 16 * wave + c;  // this lane's row
+        const int64_t row = rr < N ? rr : N - 1;
+        uint4 wv[NH][kMaxGpw];
+        uint32_t sv[NH][kMaxGpw / 4];
+#pragma unroll
+        for (int i = 0; i < kMaxGpw; ++i) {
+            const int gi = i < NG ? i : NG - 1;
+#pragma unroll
+            for (int h = 0; h < NH; ++h)
+                wv[h][i] = load_stream16(reinterpret_cast<const unsigned char*>(a.wq) + (row + h * N) * (K / 2) +
+                                         64 * gi + 16 * q);
+        }
+#pragma unroll
+        for (int i = 0; i < kMaxGpw / 4; ++i) {  // group 4 i + q
+            const int gi = 4 * i + q < NG ? 4 * i + q : NG - 1;
+#pragma unroll
+            for (int h = 0; h < NH; ++h) sv[h][i] = a.ws[(row + h * N) * NG + gi];
+        }
+        // the direct-to-LDS loads (issued first) have landed: at most the
+        // weight loads remain in flight
+        constexpr int kLoads = NH * (kMaxGpw + kMaxGpw / 4);
+        static_assert(kLoads < 64, "vmcnt range");
+        __builtin_amdgcn_s_waitcnt((kLoads & 15) | ((kLoads >> 4) << 14) | (7 << 4));
+        asm volatile("s_barrier" ::: "memory");
+        // two MFMAs per group (codes 32 q .. +15, then +16 .. +31)
+        v4i dres[NH][kMaxGpw];
+#pragma unroll
+        for (int i = 0; i < kMaxGpw; ++i) {
+            if (i >= NG) continue;
+            const v4i a0 = *reinterpret_cast<const v4i*>(xr + 128 * i);
+            const v4i a1 = *reinterpret_cast<const v4i*>(xr + 128 * i + 16);
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const v4i b0{(int)(wv[h][i].x & kNibbleMask), (int)((wv[h][i].x >> 4) & kNibbleMask),
+                             (int)(wv[h][i].y & kNibbleMask), (int)((wv[h][i].y >> 4) & kNibbleMask)};
+                const v4i b1{(int)(wv[h][i].z & kNibbleMask), (int)((wv[h][i].z >> 4) & kNibbleMask),
+                             (int)(wv[h][i].w & kNibbleMask), (int)((wv[h][i].w >> 4) & kNibbleMask)};
+                v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, v4i{0, 0, 0, 0}, 0, 0, 0);
+                dres[h][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, d, 0, 0, 0);
+            }
+        }
+        // every lane needs the (s, m) of all groups of its row: through LDS
+#pragma unroll
+        for (int i = 0; i < kMaxGpw / 4; ++i) {
+            const int gi = 4 * i + q;
+            if (gi < NG) {
+#pragma unroll
+                for (int h = 0; h < NH; ++h)
+                    sm_lds[(h * RB + 16 * wave + c) * NGP + gi] = make_float2(f16lo(sv[h][i]), f16hi(sv[h][i]));
+            }
+        }
+        __syncthreads();
+        // fp32 chains of (token 4 q + j, row) over the groups in order
+        float acc[NH][4];
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[h][j] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMaxGpw; ++i) {
+            if (i >= NG) continue;
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const float2 w = sm_lds[(h * RB + 16 * wave + c) * NGP + i];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
+                    acc[h][j] = fmaf(w.x, (float)dres[h][i][j], acc[h][j]);
+                    acc[h][j] = fmaf(w.y, (float)xs_lds[t * NG + i], acc[h][j]);
+                }
+            }
+        }
+        float v[NH][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
+#pragma unroll
+            for (int h = 0; h < NH; ++h) v[h][j] = acc[h][j] * dx_lds[t];
+        }
+        if (a.acc_dump) {  // test hook: the group sums the chains folded
+            const int rows_total = NH * (int)N;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int t = 4 * q + j;
+                if (t < a.M && rr < N)
+#pragma unroll
+                    for (int h = 0; h < NH; ++h)
+#pragma unroll
+                        for (int i = 0; i < kMaxGpw; ++i)  // constant indices: registers
+                            if (i < NG) a.acc_dump[((int64_t)t * rows_total + h * N + rr) * NG + i] = dres[h][i][j];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = 4 * q + j;
+            if (t >= a.M || rr >= N) continue;
+            if (ARGMAX) {
+                if (a.y) a.y[(int64_t)t * N + rr] = v[0][j];
+                if (v[0][j] > -3.0e38f) {
+                    const unsigned long long key = argmax_key(v[0][j], (uint32_t)rr);
+                    best[j] = key > best[j] ? key : best[j];
+                }
+            } else {
+                float* yo = a.y + (int64_t)t * N + rr;
+                if (MODE == 0) {
+                    *yo = v[0][j];
+                } else if (MODE == 1) {
+                    *yo = *yo + v[0][j];
+                } else {
+                    *yo = silu_mul(v[0][j], v[NH - 1][j]);
+                }
+            }
+        }
+    }
+    if (!ARGMAX) return;
+
+    // the workgroup's best key per token: over the wave's 16 rows by
+    // shuffles, over the 4 waves through LDS; then the cross-workgroup combine
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        unsigned long long key = best[j];
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) {
+            const unsigned long long u = __shfl_xor(key, o, 16);
+            key = u > key ? u : key;
+        }
+        if (c == 0 && 4 * q + j < MT) wbest[wave * MT + 4 * q + j] = key;
+    }
+    __syncthreads();
+    unsigned long long wb = 0;
+    if (tid < MT && tid < a.M)
+#pragma unroll
+        for (int w = 0; w < kRowsWaves; ++w) wb = wbest[w * MT + tid] > wb ? wbest[w * MT + tid] : wb;
+    argmax_combine<MT>(p.am, (int)a.M, p.nblocks, wb);
+}
+
 template <int MT, int MODE, bool ARGMAX>
 hipError_t launch_rbw(const MfmaGemvParams& gp, int rbw, size_t lds, unsigned grid, hipStream_t s) {
-    dim3 g(grid), b(256);
+    dim3 g(grid), b(64 * kWaves);
     switch (rbw) {
-        case 4: hipLaunchKernelGGL((gemv_mfma_kernel<MT, MODE, 4, ARGMAX>), g, b, lds, s, gp); break;
         case 2: hipLaunchKernelGGL((gemv_mfma_kernel<MT, MODE, 2, ARGMAX>), g, b, lds, s, gp); break;
         default: hipLaunchKernelGGL((gemv_mfma_kernel<MT, MODE, 1, ARGMAX>), g, b, lds, s, gp); break;
     }
@@ -392,10 +483,26 @@ hipError_t launch_gemv_mfma(const LinearArgs& a, const ArgmaxArgs* am, hipStream
     const int rb = 16 * rbw, nh = a.mode == 2 ? 2 : 1, mt = 8;
     const unsigned grid = (unsigned)((a.N + rb - 1) / rb);
     gp.nblocks = (int)grid;
-    // (rbw == 4: no group-sum buffer, the per-wave best keys instead)
-    const size_t lds = (rbw == kWaves ? (size_t)kWaves * mt * 8 : (size_t)mt * nh * rb * gp.NGP * 4) +
-                       (size_t)nh * rb * gp.NGP * 8 + (size_t)((mt * NG + 63) & ~63) * 4 + 64 * 4 +
-                       (size_t)mt * a.K;
+    const size_t lds = (size_t)mt * nh * rb * gp.NGP * 4 + (size_t)nh * rb * gp.NGP * 8 +
+                       (size_t)((mt * NG + 63) & ~63) * 4 + 64 * 4 + (size_t)mt * a.K;
+    if (rbw == kWaves) {  // K <= 2048: the register-chain kernel, 128 rows per workgroup
+        const int rbr = 16 * kRowsWaves;
+        const size_t lds_rows = (size_t)nh * rbr * gp.NGP * 8 + (size_t)((mt * NG + 63) & ~63) * 4 + 64 * 4 +
+                                (size_t)mt * a.K + (size_t)kRowsWaves * mt * 8;
+        const unsigned rgrid = (unsigned)((a.N + rbr - 1) / rbr);
+        gp.nblocks = (int)rgrid;
+        dim3 g(rgrid), b(64 * kRowsWaves);
+        if (am) {
+            hipLaunchKernelGGL((gemv_mfma_rows_kernel<8, 0, true>), g, b, lds_rows, s, gp);
+        } else {
+            switch (a.mode) {
+                case 0: hipLaunchKernelGGL((gemv_mfma_rows_kernel<8, 0, false>), g, b, lds_rows, s, gp); break;
+                case 1: hipLaunchKernelGGL((gemv_mfma_rows_kernel<8, 1, false>), g, b, lds_rows, s, gp); break;
+                default: hipLaunchKernelGGL((gemv_mfma_rows_kernel<8, 2, false>), g, b, lds_rows, s, gp); break;
+            }
+        }
+        return hipGetLastError();
+    }
     if (am) return launch_rbw<8, 0, true>(gp, rbw, lds, grid, s);
     switch (a.mode) {
         case 0: return launch_rbw<8, 0, false>(gp, rbw, lds, grid, s);
