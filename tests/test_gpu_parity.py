@@ -371,6 +371,10 @@ QUANT_GEMV_CASES = [
     (2, 3072, 96, 32, 0, True),      # K not a multiple of 2048, G = 32
     (1, 16384, 256, 128, 1, True),   # eight passes
     (5, 2048, 512, 128, 0, True),    # M > 2: quantiser and GEMV launches
+    (4, 2048, 3072, 128, 2, True),   # 4 tokens, gate_up
+    (8, 2048, 2048, 32, 1, False),   # 8 tokens, G = 32, += residual
+    (3, 128, 300, 128, 0, True),     # 3 tokens, one group, partial pass
+    (6, 6144, 512, 128, 1, False),
 ]
 
 
