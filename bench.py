@@ -408,8 +408,8 @@ def bench_configs(torch, lib, ops):
     from webyiq_amd.layer import DecodeLayer
     H, Q, KV, F, L = 2048, 2048, 512, 6144, 20
     step = {}
-    for M, fuse, attention in ((1, True, "combine"), (2, True, "combine"), (1, True, "copy"),
-                               (1, False, "copy")):
+    for M, fuse, attention in ((1, True, "combine"), (2, True, "combine"), (4, True, "combine"),
+                               (8, True, "combine"), (1, True, "copy"), (1, False, "copy")):
         x = torch.zeros((M, H), dtype=torch.float32, device="cuda")
         layers = []
         for _ in range(L):
@@ -433,7 +433,11 @@ def bench_configs(torch, lib, ops):
         t = graph_time(torch, [Step()], 10)
         nbw = sum(lay.weight_bytes() for lay in layers)
         key = f"M{M}" + ("" if attention == "combine" else "_copy_attn") + ("" if fuse else "_unfused")
-        step[key] = {"us_per_layer": round(t / L * 1e6, 3), "layers": L, "launches_per_layer": 5 if fuse else 9,
+        # qkv, gate_up, down: quantiser + GEMV, one launch when fused and M <= 2;
+        # o: a plain GEMV after the chunk merge, or quantiser + GEMV after the copy
+        per_pair = 1 if fuse and M <= 2 else 2
+        launches = 3 * per_pair + 1 + (1 if attention == "combine" else per_pair)
+        step[key] = {"us_per_layer": round(t / L * 1e6, 3), "layers": L, "launches_per_layer": launches,
                      "attention_stand_in": attention, "weight_GBps": round(nbw / t / 1e9, 1)}
         del layers
     res["decode_step_graph"] = step
