@@ -3,7 +3,8 @@
   python -m webyiq_amd.build          # compile every kernel + the C ABI
 
 Each .hip translation unit is compiled in parallel into webyiq_amd/_build/,
-then linked into webyiq_amd/libwebyiq_q4q8.so next to this file.  Flags:
+then linked into webyiq_amd/libwebyiq_q4q8.so next to this file; the C++ host
+side (host/webyiq_graph.cpp, g++) follows as libwebyiq_graph.so.  Flags:
   --offload-arch=gfx950 only (no other targets, no CUDA/HIP dual paths);
   -Xclang -target-feature -Xclang -packed-fp32-ops: no packed fp32 ops;
   -mllvm -amdgpu-mfma-vgpr-form: MFMA results in ordinary VGPRs, which the
@@ -21,6 +22,8 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libwebyiq_q4q8.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+HOST_LIB = os.path.join(HERE, "libwebyiq_graph.so")
+CXX = os.environ.get("CXX", "g++")
 
 SOURCES = ["capi.hip", "quant_act.hip", "gemv_q4q8.hip", "gemv_mfma.hip", "gemm_q4q8.hip", "argmax.hip", "embed.hip",
            "attn_combine.hip"]
@@ -62,7 +65,21 @@ def build(verbose=False):
     tmp = LIB + ".tmp"
     subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp], check=True)
     os.replace(tmp, LIB)
+    build_host(verbose)
     return LIB
+
+
+def build_host(verbose=False):
+    """The C++ host side (host/webyiq_graph.cpp): plain C++17 over the C ABI,
+    linked against libwebyiq_q4q8.so next to it."""
+    tmp = HOST_LIB + ".tmp"
+    cmd = [CXX, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", os.path.join(HERE, "host", "webyiq_graph.cpp"),
+           "-o", tmp, "-L" + HERE, "-lwebyiq_q4q8", "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, HOST_LIB)
+    return HOST_LIB
 
 
 if __name__ == "__main__":
