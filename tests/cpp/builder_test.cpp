@@ -91,7 +91,11 @@ static void cpu_checks() {
     ga64.ga = 64;
     expect_err(b.gemv("up", "mlp.up", K, N, 0, 1, ga64, y), "activation group 64", "GA");
     Builder b48(wts, 48);
-    expect_err(b48.gemv("up", "mlp.up", K, N, 0, 1, a, y), "quant group 48", "G");
+    expect_err(b48.gemv("up", "mlp.up", K, N, 0, 1, a, y), "up: quant group 48", "G");
+    expect_err(b48.quant("q", K, 1e-6, fake(0x90000, K * 4), nullptr, 1, a), "q: quant group 48", "G in quant");
+    // the builder owns its map: one built from a temporary stays valid
+    Builder bt({{"t.q", fake(0x10000, N * K / 2)}, {"t.s", fake(0x20000, N * (K / G) * 4)}}, G);
+    CHECK(bt.gemv("t", "t", K, N, 0, 1, a, y).is_ok(), "builder over a temporary map");
 
     // matmul dispatch by path (graph.rs:207-214): Decode/Spec -> GEMV with the
     // path's tokens, Prefill -> GEMM over m tokens

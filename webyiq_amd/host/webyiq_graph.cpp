@@ -45,8 +45,8 @@ uint32_t tokens(Path p) {
     }
 }
 
-Builder::Builder(const std::unordered_map<std::string, Buffer>& weights, int32_t group)
-    : weights_(weights), group_(group) {}
+Builder::Builder(std::unordered_map<std::string, Buffer> weights, int32_t group)
+    : weights_(std::move(weights)), group_(group) {}
 
 Result<Buffer> Builder::w(const std::string& name) const {
     auto it = weights_.find(name);
@@ -68,6 +68,7 @@ Result<Builder::Q4> Builder::q4(const std::string& w, uint32_t rows, uint32_t k)
 }
 
 std::string Builder::check_acts(const std::string& name, uint32_t k, uint32_t t, const Acts& a) const {
+    if (group_ != 32 && group_ != 128) return fmt("%s: quant group %d (32 or 128)", name.c_str(), group_);
     const uint32_t ga = a.ga == 0 ? k : a.ga;
     if (ga != k && ga != 32) return fmt("%s: activation group %u (32 or per token)", name.c_str(), ga);
     const uint32_t ge = ga < (uint32_t)group_ ? ga : (uint32_t)group_;

@@ -77,8 +77,9 @@ struct OpDef {
 class Builder {
   public:
     // weights: the engine's name -> buffer map (graph.rs:119), int4 tensors as
-    // "{w}.q" / "{w}.s" pairs; group: the manifest's quant.group
-    Builder(const std::unordered_map<std::string, Buffer>& weights, int32_t group);
+    // "{w}.q" / "{w}.s" pairs (copied: the builder keeps its own map of the
+    // caller's device pointers); group: the manifest's quant.group
+    Builder(std::unordered_map<std::string, Buffer> weights, int32_t group);
 
     // graph.rs:186-188
     Result<Buffer> w(const std::string& name) const;
@@ -116,7 +117,7 @@ class Builder {
     Result<Q4> q4(const std::string& w, uint32_t rows, uint32_t k) const;
     std::string check_acts(const std::string& name, uint32_t k, uint32_t t, const Acts& a) const;
 
-    const std::unordered_map<std::string, Buffer>& weights_;
+    std::unordered_map<std::string, Buffer> weights_;
     int32_t group_;
 };
 
