@@ -107,7 +107,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "multi-GPU sharding is described in DESIGN.md, not run", file=sys.stderr)
+              "the path shards along the output rows, but no multi-GPU run is built", file=sys.stderr)
         sys.exit(2)
     import torch
     from webyiq_amd import _lib, ops
