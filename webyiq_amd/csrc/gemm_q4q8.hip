@@ -179,7 +179,16 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     const int xcd = bid % kXcds, li = bid / kXcds;
     const int per = T / kXcds, rem = T % kXcds;
     const int lt = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + li;
-    const int tile_n = lt / p.tilesM, tile_m = lt % p.tilesM;
+    // tiles in groups of GM token tiles: the run of consecutive tiles one
+    // XCD takes spans GM token tiles x (run / GM) row tiles, so that for long
+    // rows (K >= 4096, 128 tokens x K bytes per token tile) its L2 holds the
+    // activations of 4 token tiles rather than of all of them; shorter rows
+    // keep every token tile of a row tile together (GM = tilesM)
+    const int GM = K >= 4096 ? 4 : p.tilesM;
+    const int grp = lt / (GM * p.tilesN);
+    const int gm = p.tilesM - grp * GM < GM ? p.tilesM - grp * GM : GM;
+    const int off = lt - grp * GM * p.tilesN;
+    const int tile_m = grp * GM + off % gm, tile_n = off / gm;
     const int64_t m0 = (int64_t)tile_m * BM;
     constexpr int OUTW = MODE == 2 ? BN / 2 : BN;  // output columns per tile
     const int64_t n0 = (int64_t)tile_n * OUTW;
