@@ -161,3 +161,30 @@ def test_attn_combine_argument_errors():
     assert combine(gate=A4, gs=2 * 16 * 128 - 1) == _lib.WQ_ESHAPE and "gate_stride" in err()
     assert combine(xq=ctypes.c_void_p(0x10008)) == _lib.WQ_EALIGN
     assert combine(part=ctypes.c_void_p(0x10002)) == _lib.WQ_EALIGN
+
+
+def test_last_error_is_per_thread():
+    """wq_last_error() is thread-local: two threads failing with different
+    messages, interleaved (ctypes releases the GIL around each call), each
+    read back their own."""
+    import threading
+    start = threading.Barrier(2)
+    bad = []
+
+    def worker(kind):
+        start.wait()
+        for _ in range(2000):
+            if kind == 0:
+                rc, want = gemv(K=2000), "multiple of 128"
+            else:
+                rc, want = gemv(mode=5), "unknown mode"
+            if rc >= 0 or want not in err():
+                bad.append((kind, rc, err()))
+                return
+
+    ts = [threading.Thread(target=worker, args=(k,)) for k in (0, 1)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not bad, bad[:3]
