@@ -152,6 +152,12 @@ GEMV_CASES = [
     (5, 6144, 16384, 128, None, 1),  # K split in 4
     (3, 2048, 20000, 128, None, 2),  # gate/up pairs
     (4, 4096, 16384, 128, None, 0),  # K split in 2
+    # the limits the host checks: 8 tokens x K = 16384 (8 passes) on the dot4
+    # kernel, the MFMA GEMV at its K = 8192, and K = 16384 in the
+    # reference-native format
+    (8, 16384, 512, 128, None, 1),
+    (8, 8192, 16384, 128, None, 0),
+    (1, 16384, 6144, 32, 32, 0),
 ]
 
 
