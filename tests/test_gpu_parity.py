@@ -269,6 +269,21 @@ def test_gemm_wide_tiles(K, N, G, GA, mode):
     assert np.all(np.isfinite(got))
 
 
+def test_gemm_long_rows_partial_tile_group():
+    """K >= 4096 assigns tiles to XCDs in groups of 4 token tiles; M = 640
+    has 5 token tiles, so one full group and a partial one.  Sampled tokens
+    of every token tile against the oracle."""
+    M, K, N = 640, 4096, 1024
+    note(f"gemm long rows M={M} K={K} N={N}")
+    wq, ws, x, xq, dx, xs = setup_linear(641, M, K, N, 128, None)
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, 128)
+    got = host(ops.gemm(w, dev_acts(xq, dx, xs, K, 128)))
+    idx = np.array([0, 127, 128, 255, 300, 383, 384, 511, 512, 600, 639])
+    want = orc.linear(wq, ws, K, 128, xq[idx], dx[idx], xs[idx])
+    assert rel_err(got[idx], want) < 1e-5
+    assert np.all(np.isfinite(got))
+
+
 def test_gemm_matches_gemv_rows():
     """Decode vs prefill cross-check (the reference's --ppl / --sequential
     harnesses, crates/cli/src/main.rs:209-250): each GEMM row matches the GEMV
