@@ -56,6 +56,7 @@ def setup_linear(seed, M, K, rows, G, GA):
     (5, 1024, 32, 128, False), (2, 128, None, 128, False), (64, 2048, None, 128, False),
     (4, 2048, None, 128, True), (3, 6144, 32, 32, True),
     (1, 2176, None, 32, True), (2, 10240, None, 128, True),   # partial pass; rows past 4 passes
+    (48, 4096, 32, 128, True), (40, 12288, None, 32, True),   # one wave per token: 2 and 6 passes
 ])
 def test_quant_act_bit_exact(M, K, GA, G, norm):
     note(f"quant M={M} K={K} GA={GA} G={G} norm={norm}")
