@@ -60,6 +60,7 @@ def make_part(rng, M, H, D, nch, pos, equal_max):
 
 @pytest.mark.parametrize("D,M,H,nch,pos", [
     (64, 2, 3, 8, 100), (128, 2, 4, 8, 127), (256, 1, 2, 4, 31), (128, 3, 2, 130, 4000),
+    (128, 2, 4, 8192, 262142),  # the host-checked maximum: 8192 chunks, last token at 262143
 ])
 def test_attn_combine_equal_maxima_bit_exact(D, M, H, nch, pos):
     note(f"attn_combine exact D={D} M={M} H={H} nch={nch} pos={pos}")
