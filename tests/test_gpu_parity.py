@@ -449,6 +449,24 @@ def test_embed_bit_exact(G, M):
     assert np.array_equal(x.view(np.uint32), want.view(np.uint32))
 
 
+def test_embed_full_vocabulary_edges():
+    """The lookup at the real vocabulary (151,936 rows): the first and last
+    rows, and ids V and 0xFFFFFFFF (zero rows), against the oracle."""
+    V, K, G = 151936, 2048, 128
+    note(f"embed V={V}")
+    rng = np.random.default_rng(5)
+    wq = rng.integers(0, 2**32, size=(V, K // 8), dtype=np.uint32)
+    lo = rng.integers(0x1800, 0x2400, size=(V, K // G), dtype=np.uint32)
+    hi = rng.integers(0x9800, 0xA400, size=(V, K // G), dtype=np.uint32)
+    ws = lo | (hi << 16)
+    tok = np.array([0, 1, V - 1, V - 2, V, 0xFFFFFFFF, 12345, V - 1], np.uint32)
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
+    x = host(ops.embed(w, dev(tok.view(np.int32))))
+    want = orc.embed(wq, ws, K, G, tok)
+    assert np.array_equal(x.view(np.uint32), want.view(np.uint32))
+    assert not np.any(x[4]) and not np.any(x[5])
+
+
 def test_gather_rows_and_draft_head():
     """The reduced draft lm_head (graph.rs:511-522): gather the rows of the
     ascending draft ids, then the fused lm_head + argmax over them maps the
