@@ -137,6 +137,28 @@ static void cpu_checks() {
         CHECK(r.error().rfind("up_proj: wq_gemv: wq", 0) == 0 && r.error().find("aligned") != std::string::npos,
               "encode error '%s'", r.error().c_str());
     CHECK(later == 0, "ops after a failure are not launched");
+    // the ops around the path
+    expect_err(b.embed("embed", "emb", K, 1024, 2, tok, x), "missing tensor emb.q", "embed table");
+    expect_err(b.embed("embed", "head", K, 1024, 2, tok, fake(0x90000, 2 * K * 4 - 4)), "embed: x holds", "embed x");
+    CHECK(b.embed("embed", "head", K, 1024, 2, tok, x).is_ok(), "embed builds");
+    expect_err(b.gather_rows("gather", "head", K, 1024, 8, tok, fake(0xD0000, 8 * K / 2 - 16), wsp),
+               "gather: dq holds", "gather dq");
+    Acts p32 = a;
+    p32.ga = 32;
+    p32.dx = fake(0x71000, 8 * (K / 32) * 4);
+    p32.xs = fake(0x72000, 8 * (K / 32) * 4);
+    const Buffer part = fake(0xE0000, (size_t)2 * 2 * 4 * (128 + 2) * 4);
+    CHECK(b.attn_combine("combine", part, 2, 2, 128, 4, 100, nullptr, 0, p32).is_ok(), "combine builds");
+    expect_err(b.attn_combine("combine", part, 2, 2, 96, 4, 100, nullptr, 0, p32), "head dim 96", "combine D");
+    expect_err(b.attn_combine("combine", part, 2, 2, 128, 4, 127, nullptr, 0, p32), "positions 0..128", "combine pos");
+    expect_err(b.attn_combine("combine", part, 2, 2, 128, 4, 100, nullptr, 0, a), "per-32", "combine ga");
+    expect_err(b.attn_combine("combine", part, 2, 2, 128, 5, 100, nullptr, 0, p32), "combine: part holds", "part");
+    expect_err(b.attn_combine("combine", part, 2, 2, 128, 4, 100, &x, 511, p32), "gate_stride 511", "gate stride");
+    const Buffer half = fake(0xA0000, K / 2 * 4);
+    CHECK(b.mtp_in("mtp_in", K / 2, 1e-6, x, x, half, half, half, 2, p32).is_ok(), "mtp_in builds");
+    expect_err(b.mtp_in("mtp_in", K / 2, 1e-6, x, x, half, half, half, 2, a), "per-32", "mtp_in ga");
+    expect_err(b.mtp_in("mtp_in", K / 2, 1e-6, x, x, half, half, fake(0xA0000, 8), 2, p32), "norm_h holds", "norm_h");
+
     std::vector<OpDef> fine{OpDef{"a", [&](void*) { ++later; return WQ_OK; }},
                             OpDef{"b", [&](void*) { ++later; return WQ_OK; }}};
     CHECK(encode(fine, nullptr).is_ok() && later == 2, "encode runs every op in order");
@@ -305,6 +327,88 @@ static void gpu_step(Path p, uint32_t t) {
     std::fflush(stdout);
 }
 
+// embed, the chunk merge feeding a per-32 GEMV, and the MTP input stage,
+// built with Builder and compared bit for bit with the oracle (the merge with
+// equal chunk maxima, where every chunk weight is exp(0) exactly)
+static void gpu_producers() {
+    const uint32_t K = 1024, V = 4096, N = 256, H = 4, D = 128, NCH = 8, T = 2;
+    const int G = 128;
+    const int64_t POS = 100;
+    std::mt19937 rng(77);
+    Q4Host tab = make_weight(rng, V, K, G), wo = make_weight(rng, N, H * D, G);
+    Dev d;
+    Builder b({{"embed.q", d.put(tab.q)}, {"embed.s", d.put(tab.s)}, {"o.q", d.put(wo.q)}, {"o.s", d.put(wo.s)}}, G);
+    auto acts32 = [&](uint32_t k) {
+        Acts a;
+        a.xq = d.zeros((size_t)T * k);
+        a.dx = d.zeros((size_t)T * (k / 32) * 4);
+        a.xs = d.zeros((size_t)T * (k / 32) * 4);
+        a.ga = 32;
+        return a;
+    };
+    // embed
+    const std::vector<uint32_t> tok{7, V + 3};
+    const Buffer dtok = d.put(tok), x = d.zeros((size_t)T * K * 4);
+    // chunk partials [T, H, NCH, D + 2]: NaN past each token's chunks
+    std::normal_distribution<float> nd(0.0f, 3.0f);
+    std::uniform_real_distribution<float> ud(1.0f, 32.0f);
+    std::vector<float> part((size_t)T * H * NCH * (D + 2), std::nanf(""));
+    for (uint32_t m = 0; m < T; ++m)
+        for (uint32_t h = 0; h < H; ++h)
+            for (uint32_t c = 0; c < (POS + m + 32) / 32; ++c) {
+                float* p = &part[(((size_t)m * H + h) * NCH + c) * (D + 2)];
+                for (uint32_t i = 0; i < D; ++i) p[i] = nd(rng);
+                p[D] = 0.75f;
+                p[D + 1] = ud(rng);
+            }
+    const Acts ao = acts32(H * D);
+    const Buffer y = d.zeros((size_t)T * N * 4);
+    // MTP input
+    std::normal_distribution<float> n1(0.0f, 1.0f), nw(1.0f, 0.1f);
+    std::vector<float> emb((size_t)T * K), hid((size_t)T * K), nf(K), ne(K), nh(K);
+    for (float& v : emb) v = n1(rng);
+    for (float& v : hid) v = n1(rng);
+    for (auto* w : {&nf, &ne, &nh})
+        for (float& v : *w) v = nw(rng);
+    const Acts am = acts32(2 * K);
+
+    std::vector<OpDef> ops;
+    auto add = [&](Result<OpDef> r) {
+        CHECK(r.is_ok(), "build: %s", r.error().c_str());
+        if (r.is_ok()) ops.push_back(r.value());
+    };
+    add(b.embed("embed", "embed", K, V, T, dtok, x));
+    add(b.attn_combine("attn_combine", d.put(part), T, H, D, NCH, POS, nullptr, 0, ao));
+    add(b.gemv("o_proj", "o", H * D, N, WQ_MODE_STORE, T, ao, y));
+    add(b.mtp_in("mtp_in", K, 1e-6, d.put(emb), d.put(hid), d.put(nf), d.put(ne), d.put(nh), T, am));
+    auto r = encode(ops, nullptr);
+    CHECK(r.is_ok(), "encode: %s", r.error().c_str());
+    HIP_OK(hipDeviceSynchronize());
+
+    std::vector<float> xw((size_t)T * K);
+    or_embed(tab.q.data(), tab.s.data(), V, K, G, tok.data(), T, xw.data());
+    CHECK(same_bits(get<float>(x, xw.size()), xw), "embed");
+    const uint32_t KO = H * D;
+    std::vector<int8_t> cq((size_t)T * KO);
+    std::vector<float> cd((size_t)T * KO / 32), yo((size_t)T * N);
+    std::vector<int32_t> cs((size_t)T * KO / 32);
+    or_attn_combine(part.data(), T, H, D, NCH, POS, nullptr, 0, cq.data(), cd.data(), cs.data());
+    CHECK(same_bits(get<int8_t>(ao.xq, cq.size()), cq), "attn_combine codes");
+    CHECK(same_bits(get<float>(ao.dx, cd.size()), cd), "attn_combine scales");
+    CHECK(same_bits(get<int32_t>(ao.xs, cs.size()), cs), "attn_combine sums");
+    or_linear(wo.q.data(), wo.s.data(), N, KO, G, cq.data(), cd.data(), cs.data(), T, 32, 0, yo.data());
+    CHECK(same_bits(get<float>(y, yo.size()), yo), "o projection on per-32 activations");
+    std::vector<int8_t> mq((size_t)T * 2 * K);
+    std::vector<float> md((size_t)T * 2 * K / 32);
+    std::vector<int32_t> ms((size_t)T * 2 * K / 32);
+    or_mtp_in(emb.data(), hid.data(), nf.data(), ne.data(), nh.data(), 1e-6f, T, K, mq.data(), md.data(), ms.data());
+    CHECK(same_bits(get<int8_t>(am.xq, mq.size()), mq), "mtp_in codes");
+    CHECK(same_bits(get<float>(am.dx, md.size()), md), "mtp_in scales");
+    CHECK(same_bits(get<int32_t>(am.xs, ms.size()), ms), "mtp_in sums");
+    std::printf("  embed, attn_combine -> o_proj, mtp_in: %zu ops replayed, compared with the oracle\n", ops.size());
+    std::fflush(stdout);
+}
+
 static void gpu_checks() {
     int n = 0;
     HIP_OK(hipGetDeviceCount(&n));
@@ -315,6 +419,7 @@ static void gpu_checks() {
     gpu_step(Path::Decode, 1);
     gpu_step(Path::Spec, 2);
     gpu_step(Path::Prefill, 128);
+    gpu_producers();
 }
 
 int main(int argc, char** argv) {

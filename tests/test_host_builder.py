@@ -13,7 +13,9 @@ tests/cpp/builder_test.cpp does the checking; these tests run it.
          every intermediate compared with the CPU oracle: bit for bit, except
          the silu * up output (device expf) and the Prefill GEMM's per-token
          G = 128 output (min term folded on an f16 MFMA), both within rel
-         1e-5, the tolerance of the kernels' own parity tests.
+         1e-5, the tolerance of the kernels' own parity tests; then embed,
+         the chunk merge feeding a per-32 o projection and the MTP input
+         stage (graph.rs:439-443, 289-291, 500-504), bit for bit.
 """
 import os
 import shutil

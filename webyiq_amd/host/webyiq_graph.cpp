@@ -194,6 +194,86 @@ Result<std::vector<OpDef>> Builder::head_ops(const std::string& head, uint32_t k
     return R::ok(std::move(ops));
 }
 
+Result<OpDef> Builder::embed(const std::string& name, const std::string& table, uint32_t k, uint32_t v, uint32_t t,
+                             Buffer tok, Buffer x) {
+    std::string e = check_kn(name, k, v, 0);
+    if (e.empty() && t == 0) e = fmt("%s: 0 tokens", name.c_str());
+    if (e.empty()) e = check_size(name, "tok", tok, (size_t)t * 4);
+    if (e.empty()) e = check_size(name, "x", x, (size_t)t * k * 4);
+    if (!e.empty()) return Result<OpDef>::err(e);
+    auto wt = q4(table, v, k);
+    if (!wt.is_ok()) return Result<OpDef>::err(wt.error());
+    const Q4 q = wt.value();
+    const int32_t g = group_;
+    return Result<OpDef>::ok(OpDef{name, [=](void* s) {
+        return wq_embed(s, (const uint32_t*)q.q.ptr, (const uint32_t*)q.s.ptr, v, k, g, (const uint32_t*)tok.ptr, t,
+                        (float*)x.ptr);
+    }});
+}
+
+Result<OpDef> Builder::gather_rows(const std::string& name, const std::string& table, uint32_t k, uint32_t v,
+                                   uint32_t r, Buffer ids, Buffer dq, Buffer ds) {
+    std::string e = check_kn(name, k, v, 0);
+    if (e.empty() && r == 0) e = fmt("%s: 0 rows", name.c_str());
+    if (e.empty() && group_ != 32 && group_ != 128) e = fmt("%s: quant group %d (32 or 128)", name.c_str(), group_);
+    if (e.empty()) e = check_size(name, "ids", ids, (size_t)r * 4);
+    if (e.empty()) e = check_size(name, "dq", dq, (size_t)r * k / 2);
+    if (e.empty()) e = check_size(name, "ds", ds, (size_t)r * (k / group_) * 4);
+    if (!e.empty()) return Result<OpDef>::err(e);
+    auto wt = q4(table, v, k);
+    if (!wt.is_ok()) return Result<OpDef>::err(wt.error());
+    const Q4 q = wt.value();
+    const int32_t g = group_;
+    return Result<OpDef>::ok(OpDef{name, [=](void* s) {
+        return wq_gather_rows(s, (const uint32_t*)q.q.ptr, (const uint32_t*)q.s.ptr, v, k, g,
+                              (const uint32_t*)ids.ptr, r, (uint32_t*)dq.ptr, (uint32_t*)ds.ptr);
+    }});
+}
+
+Result<OpDef> Builder::attn_combine(const std::string& name, Buffer part, uint32_t t, uint32_t h, uint32_t d,
+                                    uint32_t nch, int64_t pos, const Buffer* gate, int64_t gate_stride,
+                                    const Acts& a) {
+    std::string e;
+    if (d != 64 && d != 128 && d != 256) e = fmt("%s: head dim %u (64, 128 or 256)", name.c_str(), d);
+    if (e.empty() && (t == 0 || h == 0 || nch == 0)) e = fmt("%s: empty shape", name.c_str());
+    if (e.empty() && (pos < 0 || pos + t - 1 >= 32 * (int64_t)nch))
+        e = fmt("%s: positions 0..%lld exceed the %u chunks", name.c_str(), (long long)(pos + t - 1), nch);
+    if (e.empty() && a.ga != 32) e = fmt("%s: the chunk merge writes per-32 activations (ga = 32)", name.c_str());
+    if (e.empty()) e = check_size(name, "part", part, (size_t)t * h * nch * (d + 2) * 4);
+    if (e.empty() && gate) {
+        if (gate_stride < 2 * (int64_t)h * d) e = fmt("%s: gate_stride %lld < 2 h d", name.c_str(), (long long)gate_stride);
+        else e = check_size(name, "gate", *gate, ((size_t)(t - 1) * gate_stride + 2 * (size_t)h * d) * 4);
+    }
+    if (e.empty()) e = check_acts(name, h * d, t, a);
+    if (!e.empty()) return Result<OpDef>::err(e);
+    const void* gp = gate ? gate->ptr : nullptr;
+    const Acts out = a;
+    return Result<OpDef>::ok(OpDef{name, [=](void* s) {
+        return wq_attn_combine(s, (const float*)part.ptr, t, h, d, nch, pos, (const float*)gp, gate_stride,
+                               (int8_t*)out.xq.ptr, (float*)out.dx.ptr, (int32_t*)out.xs.ptr);
+    }});
+}
+
+Result<OpDef> Builder::mtp_in(const std::string& name, uint32_t k, double eps, Buffer emb, Buffer x, Buffer norm_f,
+                              Buffer norm_e, Buffer norm_h, uint32_t t, const Acts& a) {
+    std::string e = check_kn(name, k, 1, 0);
+    if (e.empty() && t == 0) e = fmt("%s: 0 tokens", name.c_str());
+    if (e.empty() && a.ga != 32) e = fmt("%s: the MTP input is per-32 activations (ga = 32)", name.c_str());
+    if (e.empty()) e = check_size(name, "emb", emb, (size_t)t * k * 4);
+    if (e.empty()) e = check_size(name, "x", x, (size_t)t * k * 4);
+    if (e.empty()) e = check_size(name, "norm_f", norm_f, (size_t)k * 4);
+    if (e.empty()) e = check_size(name, "norm_e", norm_e, (size_t)k * 4);
+    if (e.empty()) e = check_size(name, "norm_h", norm_h, (size_t)k * 4);
+    if (e.empty()) e = check_acts(name, 2 * k, t, a);
+    if (!e.empty()) return Result<OpDef>::err(e);
+    const Acts out = a;
+    return Result<OpDef>::ok(OpDef{name, [=](void* s) {
+        return wq_mtp_in(s, (const float*)emb.ptr, (const float*)x.ptr, (const float*)norm_f.ptr,
+                         (const float*)norm_e.ptr, (const float*)norm_h.ptr, (float)eps, t, k, (int8_t*)out.xq.ptr,
+                         (float*)out.dx.ptr, (int32_t*)out.xs.ptr);
+    }});
+}
+
 Result<Unit> encode(const std::vector<OpDef>& ops, void* stream) {
     for (const OpDef& op : ops) {
         const int rc = op.launch(stream);

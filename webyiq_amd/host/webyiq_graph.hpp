@@ -110,6 +110,25 @@ class Builder {
                                         Buffer x, Buffer norm, const Acts& a, const Buffer* ids, Buffer tok,
                                         Buffer workspace, const Buffer* logits = nullptr);
 
+    // the other ops around the path (the survey's next rows):
+    // int4 embedding lookup of t token ids into x [t, k] (graph.rs:439-443);
+    // ids outside [0, v) give zero rows
+    Result<OpDef> embed(const std::string& name, const std::string& table, uint32_t k, uint32_t v, uint32_t t,
+                        Buffer tok, Buffer x);
+    // the draft head's packed rows: dst row r = row ids[r] of table
+    // (graph.rs:511-516); dq / ds hold r rows of the packed format
+    Result<OpDef> gather_rows(const std::string& name, const std::string& table, uint32_t k, uint32_t v,
+                              uint32_t r, Buffer ids, Buffer dq, Buffer ds);
+    // flash-decoding chunk merge of t tokens x h heads of d dims over nch
+    // chunks, positions up to pos + t - 1, optional output gate rows, into
+    // per-32 int8 activations of k = h d (graph.rs:289-291); a.ga must be 32
+    Result<OpDef> attn_combine(const std::string& name, Buffer part, uint32_t t, uint32_t h, uint32_t d,
+                               uint32_t nch, int64_t pos, const Buffer* gate, int64_t gate_stride, const Acts& a);
+    // MTP input stage: per-32 int8 activations [t, 2k] of the normed
+    // embedding and hidden state (graph.rs:500-504); a.ga must be 32
+    Result<OpDef> mtp_in(const std::string& name, uint32_t k, double eps, Buffer emb, Buffer x, Buffer norm_f,
+                         Buffer norm_e, Buffer norm_h, uint32_t t, const Acts& a);
+
   private:
     struct Q4 {
         Buffer q, s;
