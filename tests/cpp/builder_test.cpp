@@ -381,6 +381,10 @@ static void gpu_producers() {
     add(b.attn_combine("attn_combine", d.put(part), T, H, D, NCH, POS, nullptr, 0, ao));
     add(b.gemv("o_proj", "o", H * D, N, WQ_MODE_STORE, T, ao, y));
     add(b.mtp_in("mtp_in", K, 1e-6, d.put(emb), d.put(hid), d.put(nf), d.put(ne), d.put(nh), T, am));
+    // draft-head rows: two in range, one past the table (zero rows)
+    const std::vector<uint32_t> gids{3, V - 1, V};
+    const Buffer dq = d.zeros((size_t)3 * K / 2), ds = d.zeros((size_t)3 * (K / G) * 4);
+    add(b.gather_rows("gather_rows", "embed", K, V, 3, d.put(gids), dq, ds));
     auto r = encode(ops, nullptr);
     CHECK(r.is_ok(), "encode: %s", r.error().c_str());
     HIP_OK(hipDeviceSynchronize());
@@ -405,7 +409,17 @@ static void gpu_producers() {
     CHECK(same_bits(get<int8_t>(am.xq, mq.size()), mq), "mtp_in codes");
     CHECK(same_bits(get<float>(am.dx, md.size()), md), "mtp_in scales");
     CHECK(same_bits(get<int32_t>(am.xs, ms.size()), ms), "mtp_in sums");
-    std::printf("  embed, attn_combine -> o_proj, mtp_in: %zu ops replayed, compared with the oracle\n", ops.size());
+    const std::vector<uint32_t> gq = get<uint32_t>(dq, 3 * K / 8), gs = get<uint32_t>(ds, 3 * (K / G));
+    bool rows_ok = true;
+    for (int r = 0; r < 3; ++r)
+        for (uint32_t i = 0; i < K / 8; ++i)
+            rows_ok &= gq[r * (K / 8) + i] == (r < 2 ? tab.q[(size_t)gids[r] * (K / 8) + i] : 0u);
+    for (int r = 0; r < 3; ++r)
+        for (uint32_t i = 0; i < K / G; ++i)
+            rows_ok &= gs[r * (K / G) + i] == (r < 2 ? tab.s[(size_t)gids[r] * (K / G) + i] : 0u);
+    CHECK(rows_ok, "gather_rows");
+    std::printf("  embed, attn_combine -> o_proj, mtp_in, gather_rows: %zu ops replayed, compared with the oracle\n",
+                ops.size());
     std::fflush(stdout);
 }
 
