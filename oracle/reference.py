@@ -13,7 +13,6 @@ Restates:
 Seeded inputs follow the benchmark protocol: numpy default_rng(seed);
 W ~ N(0, 0.02); x ~ N(0, 1) with 8 outlier channels scaled by 20.
 """
-import os
 import time
 
 import numpy as np
@@ -97,8 +96,8 @@ def argmax_ref(logits):
 
 
 def time_cpu(fn, warmup=3, iters=20, max_seconds=30.0):
-    """Median wall time (s) of fn() after warm-up, bounded to max_seconds of work."""
-    torch.set_num_threads(os.cpu_count() or 1)
+    """Median wall time (s) of fn() after warm-up, bounded to max_seconds of
+    work, on the torch thread count the caller set (torch.get_num_threads())."""
     for _ in range(warmup):
         fn()
     ts = []

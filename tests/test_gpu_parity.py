@@ -11,6 +11,8 @@ Bars (stated per test):
     rel 1e-5 (max-norm) of the oracle;
   * every fp32 output within rel 1e-3 (max-norm) of the torch fake-quant path.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -47,6 +49,22 @@ def setup_linear(seed, M, K, rows, G, GA):
     x = ref.make_activations(rng, M, K)
     xq, dx, xs = orc.quant_act(x, GA, G)
     return wq, ws, x, xq, dx, xs
+
+
+def oracle_linear_tokens(wq, ws, K, G, xq, dx, xs, mode=0, y=None, GA=None, threads=16):
+    """orc.linear over token slices in a thread pool (the C oracle releases
+    the GIL), for checks of every token of a prefill-sized product."""
+    from concurrent.futures import ThreadPoolExecutor
+    M = xq.shape[0]
+    n = max(1, min(threads, os.cpu_count() or 1, M))
+    cuts = np.linspace(0, M, n + 1).astype(int)
+
+    def part(i):
+        a, b = cuts[i], cuts[i + 1]
+        return orc.linear(wq, ws, K, G, xq[a:b], dx[a:b], xs[a:b], mode=mode,
+                          y=None if y is None else y[a:b], GA=GA)
+    with ThreadPoolExecutor(n) as ex:
+        return np.concatenate(list(ex.map(part, range(n))), 0)
 
 
 # ------------------------------------------------------------- quantiser ----
@@ -190,6 +208,41 @@ def test_gemv_bit_exact(M, K, N, G, GA, mode):
     assert rel_err(got, fq) < 1e-3
 
 
+# MTP speculative verify: the 7 linear shapes of one
+# 2B-style layer at M = 2, 4, 8 -- q (2048 -> 2048), k and v (2048 -> 512),
+# o (2048 -> 2048, += residual), gate and up (2048 -> 6144, as two plain
+# products and as the fused gate_up pair), down (6144 -> 2048, += residual)
+VERIFY_SHAPES = [("q", 2048, 2048, 0), ("k_v", 2048, 512, 0), ("o", 2048, 2048, 1),
+                 ("gate_or_up", 2048, 6144, 0), ("gate_up", 2048, 6144, 2), ("down", 6144, 2048, 1)]
+
+
+@pytest.mark.parametrize("M", [2, 4, 8])
+@pytest.mark.parametrize("name,K,N,mode", VERIFY_SHAPES)
+def test_cfg3_verify_shapes(M, name, K, N, mode):
+    """Every (M, K x N) pair of configs[2] at group 128, per-token int8: int32
+    group sums bit-exact, fp32 bit-exact against the oracle (mode 2 within
+    rel 1e-5: device expf), within rel 1e-3 of the torch fake-quant path."""
+    note(f"cfg3 {name} M={M} K={K} N={N} mode={mode}")
+    G = 128
+    rows = 2 * N if mode == 2 else N
+    wq, ws, x, xq, dx, xs = setup_linear(M * 7919 + K + N + mode, M, K, rows, G, None)
+    y0 = np.random.default_rng(M + N).normal(size=(M, N)).astype(np.float32) if mode == 1 else None
+    want = orc.linear(wq, ws, K, G, xq, dx, xs, mode=mode, y=y0)
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
+    a = dev_acts(xq, dx, xs, K, G)
+    y, acc = ops.group_sums(ops.PATH_SPEC, w, a, mode=mode, y=dev(y0) if mode == 1 else None)
+    assert np.array_equal(host(acc), orc.group_acc(wq, K, G, xq))
+    got = host(y)
+    if mode == 2:
+        assert rel_err(got, want) < 1e-5
+    else:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    y2 = host(ops.gemv(w, a, mode=mode, y=dev(y0) if mode == 1 else None))
+    assert np.array_equal(y2.view(np.uint32), got.view(np.uint32))
+    fq = ref.FakeQuantLinear(wq, ws, K, G, mode=mode)(x, y0).numpy()
+    assert rel_err(got, fq) < 1e-3
+
+
 # ------------------------------------------------------------------ GEMM ----
 
 GEMM_CASES = [
@@ -249,8 +302,10 @@ WIDE_CASES = [
 
 @pytest.mark.parametrize("K,N,G,GA,mode", WIDE_CASES)
 def test_gemm_wide_tiles(K, N, G, GA, mode):
-    """Prefill shapes (M = 1024) on the production tile widths, checked on 24
-    sampled tokens that span every tile row against the oracle."""
+    """Prefill shapes (M = 1024) on the production tile widths against the
+    oracle: every row of the first and the last 128-token tile, and one row
+    of every 8-row group of the other tiles (row 8 g + tile index), so each
+    (wave, subtile, row group, lane) position of the tile layout is read."""
     M = 1024
     note(f"gemm wide M={M} K={K} N={N} G={G} GA={GA} mode={mode}")
     rows = 2 * N if mode == 2 else N
@@ -260,14 +315,44 @@ def test_gemm_wide_tiles(K, N, G, GA, mode):
     w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
     a = dev_acts(xq, dx, xs, gaa, G)
     got = host(ops.gemm(w, a, mode=mode, y=dev(y0) if mode == 1 else None))
-    idx = np.unique(np.concatenate([np.arange(0, M, 64), np.arange(63, M, 128)]))
-    want = orc.linear(wq, ws, K, G, xq[idx], dx[idx], xs[idx], mode=mode,
-                      y=y0[idx] if mode == 1 else None, GA=gaa)
+    idx = np.unique(np.concatenate([np.arange(0, 128), np.arange(M - 128, M),
+                                    np.arange(0, M, 8) + (np.arange(0, M, 8) // 128) % 8]))
+    want = oracle_linear_tokens(wq, ws, K, G, xq[idx], dx[idx], xs[idx], mode=mode,
+                                y=y0[idx] if mode == 1 else None, GA=gaa)
     if mode == 2 or (G == 128 and GA is None):
         assert rel_err(got[idx], want) < 1e-5
     else:
         assert np.array_equal(got[idx].view(np.uint32), want.view(np.uint32))
     assert np.all(np.isfinite(got))
+
+
+@pytest.mark.parametrize("K,N", [(2048, 6144), (6144, 2048)])
+def test_gemm_prefill_production_int32(K, N):
+    """BASELINE configs[3] on the production kernel (the tile width the
+    launcher picks for M = 1024, not a debug instance): the int32 group sums
+    of all 1,024 tokens bit-exact against an exact integer reference (one
+    float64 product per group, exact for these magnitudes), and the fp32
+    output of all 1,024 tokens within rel 1e-5 of the oracle."""
+    M, G = 1024, 128
+    note(f"gemm production int32 M={M} K={K} N={N}")
+    wq, ws, x, xq, dx, xs = setup_linear(K * 3 + N, M, K, N, G, None)
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
+    a = dev_acts(xq, dx, xs, K, G)
+    y, acc = ops.group_sums(ops.PATH_PREFILL, w, a)
+    got_acc = host(acc)
+    q = orc.q4_unpack(wq, K).astype(np.float64)
+    xf = xq.astype(np.float64)
+    for g in range(K // G):
+        sl = slice(g * G, (g + 1) * G)
+        exact = xf[:, sl] @ q[:, sl].T
+        assert np.array_equal(got_acc[:, :, g], exact.astype(np.int32)), f"group {g}"
+    del got_acc, acc
+    got = host(y)
+    want = oracle_linear_tokens(wq, ws, K, G, xq, dx, xs)
+    assert rel_err(got, want) < 1e-5
+    # the plain entry point runs the same kernel and gives the same bits
+    y2 = host(ops.gemm(w, a))
+    assert np.array_equal(y2.view(np.uint32), got.view(np.uint32))
 
 
 def test_gemm_long_rows_partial_tile_group():

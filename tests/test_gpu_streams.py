@@ -66,3 +66,36 @@ def test_two_threads_two_streams():
     for t in ts:
         t.join()
     assert not errors, errors
+
+
+@pytest.mark.gpu
+def test_non_current_stream_temporaries():
+    """Ops called with stream= a stream that is not current: the default
+    lm_head workspace (freed when the call returns) and the outputs are
+    allocated on that stream, so the current stream's allocations cannot
+    reuse them while the kernels are still queued.  Between the calls the
+    current stream allocates and fills blocks of the workspace's size with
+    ones; a reused, unzeroed workspace would corrupt the tokens."""
+    import torch
+    from webyiq_amd import ops
+
+    print("[case] ops on a non-current stream, default workspace", flush=True)
+    wq, ws, hq, hs, x, xq, y_want, tok_want = case(13)
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
+    h = ops.Q4Tensor.from_numpy(hq, hs, K, G)
+    xd = torch.from_numpy(x).cuda()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    nbytes = ops._lib.load().wq_lm_head_workspace_bytes()
+    outs, junk = [], []
+    for _ in range(ITERS):
+        a = ops.quant(xd, G=G, stream=st)
+        y = ops.gemv(w, a, stream=st)
+        tok = ops.lm_head_argmax(h, a, stream=st)
+        outs.append((a.xq, y, tok))
+        junk.append(torch.ones(nbytes, dtype=torch.uint8, device="cuda"))
+    torch.cuda.synchronize()
+    for xq_d, y_d, tok_d in outs:
+        assert np.array_equal(xq_d.cpu().numpy(), xq)
+        assert np.array_equal(y_d.cpu().numpy().view(np.uint32), y_want.view(np.uint32))
+        assert np.array_equal(tok_d.cpu().numpy().astype(np.uint32), tok_want)

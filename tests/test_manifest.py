@@ -71,6 +71,10 @@ def test_shard_bytes(tmp_path):
     (lambda d: d["tensors"]["norm"].update(shard=99), "not in the shard list"),
     (lambda d: d["tensors"]["l0.o.q"].update(shape=[256, 200], bytes=25600), "multiple of 128"),
     (lambda d: d["tensors"]["norm"].update(dtype="bf16"), "unknown dtype"),
+    # scale words that do not pair with their packed weight at the group
+    (lambda d: d["tensors"]["l0.o.s"].update(shape=[256, 8], bytes=8192), "does not match"),
+    (lambda d: d["tensors"].pop("l0.o.s"), "no q4s scale tensor"),
+    (lambda d: d["tensors"]["l0.o.q"].update(dtype="u32", bytes=4 * 256 * 256), "without a q4 tensor"),
 ])
 def test_manifest_errors(tmp_path, edit, msg):
     m, _ = write(tmp_path, layers=1)

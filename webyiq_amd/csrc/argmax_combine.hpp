@@ -34,13 +34,37 @@ __device__ __forceinline__ unsigned long long block_best(const unsigned long lon
 }
 
 // Every workgroup calls this once with its best key for token tid in
-// threads tid < M (0 elsewhere).  No memory fence is used (a device-scope
-// release would write back the XCD's L2): keys and tickets live in
-// kArgmaxSlots cache lines; a workgroup's atomicMax returns before its
-// ticket is taken, and both are device-coherent atomics, so a ticket implies
-// the max landed.  The last workgroup of each slot takes a top ticket; the
-// last of those reduces the slots, writes the token (mapped through ids when
-// set) and clears the workspace for the next call.
+// threads tid < M (0 elsewhere).  Keys and tickets live in kArgmaxSlots
+// cache lines; the last workgroup of each slot takes a top ticket; the last
+// of those reduces the slots, writes the token (mapped through ids when set)
+// and clears the workspace for the next call.
+//
+// Ordering without release fences.  A release fence at agent scope writes
+// back the whole L2 of the workgroup's XCD (the 8 XCDs' L2s are not coherent
+// with one another); one per workgroup cost 225 us on the 151,936-row head.
+// The combine instead orders its accesses by completion:
+//  1. Every access to the workspace is an agent-scope atomic (atomicMax and
+//     atomicAdd on device memory, and __hip_atomic_load/store with
+//     __HIP_MEMORY_SCOPE_AGENT).  gfx950 performs these at the device's
+//     coherence point, past the XCD-local L2, not in a per-XCD copy.
+//  2. A returning atomic delivers its value only after it has been performed
+//     there.  The keys' atomicMax results are consumed (the empty asm below)
+//     before the barrier, so thread 0's ticket atomicAdd is issued only after
+//     every key update of its workgroup has been performed.
+//  3. The ticket counts are a total order on each counter.  The workgroup
+//     that reads in_slot - 1 from its slot's counter issued its top-counter
+//     atomicAdd after every other workgroup of the slot had performed its
+//     ticket, hence (by 2) its keys; the same holds one level up for the
+//     workgroup that reads used - 1 from the top counter.
+//  4. That last workgroup then reads the keys with agent-scope atomic loads,
+//     issued after its own top ticket returned, so each load is performed
+//     after every key update, at the same coherence point.
+// The HIP memory model guarantees visibility only through release/acquire
+// pairs, so points 1, 2 and 4 rest on this hardware's completion order rather
+// than on the language model.  The last workgroup adds an agent-scope
+// acquire fence before its loads (one L2 invalidate on one XCD, not
+// measurable at these sizes), so no stale line of its XCD's L2 can be read
+// even if a key load were served from the L2.
 template <int MT>
 __device__ __forceinline__ void argmax_combine(const ArgmaxArgs& am, int M, int nblocks, unsigned long long best) {
     __shared__ unsigned int last_block;
@@ -65,6 +89,7 @@ __device__ __forceinline__ void argmax_combine(const ArgmaxArgs& am, int M, int 
     }
     __syncthreads();
     if (last_block) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         // every slot key read at once (independent device-coherent loads),
         // then reduced in LDS
         for (int o = tid; o < used * MT; o += nthreads)

@@ -617,9 +617,15 @@ hipError_t launch_tile(const LinearArgs& a, hipStream_t s) {
     gp.tilesN = (int)((a.N + outw - 1) / outw);
     gp.NE = (int)(a.K / ge);
     gp.NG = (int)(a.K / a.G);
-    if (a.G == 128)
-        return pt ? launch_mode<BN, 128, true, DUMP>(gp, s) : launch_mode<BN, 128, false, DUMP>(gp, s);
-    return pt ? launch_mode<BN, 32, true, DUMP>(gp, s) : launch_mode<BN, 32, false, DUMP>(gp, s);
+    if (a.G == 128 && pt) return launch_mode<BN, 128, true, DUMP>(gp, s);
+    // the group-sum dump of the other formats runs widths up to 128 only
+    // (launch_gemm); wider dump instances are not built
+    if constexpr (DUMP && BN > 128) {
+        return hipErrorInvalidConfiguration;
+    } else {
+        if (a.G == 128) return launch_mode<BN, 128, false, DUMP>(gp, s);
+        return pt ? launch_mode<BN, 32, true, DUMP>(gp, s) : launch_mode<BN, 32, false, DUMP>(gp, s);
+    }
 }
 
 // Widest weight tile that still gives every CU a tile (MI355X: 256 CUs), the
@@ -634,22 +640,27 @@ int pick_bn(const LinearArgs& a) {
     return 64;
 }
 
+template <bool DUMP>
 hipError_t launch_bn(const LinearArgs& a, hipStream_t s) {
     switch (pick_bn(a)) {
-        case 256: return launch_tile<256, false>(a, s);
-        case 192: return launch_tile<192, false>(a, s);
-        case 128: return launch_tile<128, false>(a, s);
-        default: return launch_tile<64, false>(a, s);
+        case 256: return launch_tile<256, DUMP>(a, s);
+        case 192: return launch_tile<192, DUMP>(a, s);
+        case 128: return launch_tile<128, DUMP>(a, s);
+        default: return launch_tile<64, DUMP>(a, s);
     }
 }
 
 }  // namespace
 
-// The group-sum dump (a test hook) runs the narrowest tiles: same kernels and
-// operand paths, fewer registers for the extra stores.
+// The group-sum dump (a test hook) of the per-token group-128 format runs the
+// tile width the production launch picks for the same shape, so the sums it
+// stores are those of the kernel instance that serves the call.  The other
+// formats dump from the narrow widths (64, or 128 for gate/up pairs): their
+// wide dump instances exceed the register file.
 hipError_t launch_gemm(const LinearArgs& a, hipStream_t s) {
-    if (a.acc_dump) return a.mode == 2 ? launch_tile<128, true>(a, s) : launch_tile<64, true>(a, s);
-    return launch_bn(a, s);
+    if (!a.acc_dump) return launch_bn<false>(a, s);
+    if (a.GA == a.K && a.G == 128) return launch_bn<true>(a, s);
+    return a.mode == 2 ? launch_tile<128, true>(a, s) : launch_tile<64, true>(a, s);
 }
 
 }  // namespace wq

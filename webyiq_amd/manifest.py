@@ -81,6 +81,25 @@ class Manifest:
                 raise ValueError(f"{name}: shape {t.shape} is not [N, K] with K a multiple of {G}")
             if t.dtype == "q4s" and len(t.shape) != 2:
                 raise ValueError(f"{name}: shape {t.shape} is not [N, K/G]")
+        # every packed weight X.q pairs with its scale words X.s of shape
+        # [N, K/G] for the manifest's group, and every X.s with an X.q: the
+        # kernels read K/G words per row of .s with no bound of their own
+        for name, t in m.tensors.items():
+            if t.dtype == "q4":
+                if not name.endswith(".q"):
+                    raise ValueError(f"{name}: a q4 tensor must be named <weight>.q")
+                sname = name[:-2] + ".s"
+                s = m.tensors.get(sname)
+                if s is None or s.dtype != "q4s":
+                    raise ValueError(f"{name}: no q4s scale tensor {sname}")
+                want = [t.shape[0], t.shape[1] // G]
+                if list(s.shape) != want:
+                    raise ValueError(f"{sname}: shape {s.shape} does not match {name} {t.shape} "
+                                     f"at group {G} (want {want})")
+            elif t.dtype == "q4s":
+                qname = name[:-2] + ".q" if name.endswith(".s") else None
+                if qname is None or qname not in m.tensors or m.tensors[qname].dtype != "q4":
+                    raise ValueError(f"{name}: scale words without a q4 tensor <weight>.q")
         return m
 
     @property
