@@ -157,6 +157,24 @@ int wq_lm_head_argmax(void* stream, const uint32_t* wq, const uint32_t* ws, int6
                       float* logits, uint32_t* tok_out, void* workspace,
                       size_t workspace_bytes);
 
+/*
+ * wq_lm_head_argmax without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * cross-workgroup reduction runs in the library's own static device array of
+ * wq_lm_head_workspace_bytes() bytes, one per GPU, held until the process
+ * ends; its address is looked up on the first call per device.  Nothing is
+ * allocated.  The array starts zeroed and every call leaves it zeroed.
+ * Calls that overlap on one GPU (concurrent streams, or threads) race on the
+ * array and must not be issued; use wq_lm_head_argmax with one workspace per
+ * stream for that.  Limits: M <= 8 tokens (as wq_lm_head_argmax); other
+ * arguments and the result as wq_lm_head_argmax.
+ */
+int wq_lm_head_argmax_noalloc(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t V,
+                              int64_t K, int32_t G, const int8_t* xq, const float* dx,
+                              const int32_t* xs, int64_t M, int32_t GA, const uint32_t* ids,
+                              float* logits, uint32_t* tok_out);
+
 /* Bytes of workspace wq_lm_head_argmax needs (no counterpart in the
  * reference, whose argmax runs as a separate single-workgroup dispatch). */
 size_t wq_lm_head_workspace_bytes(void);

@@ -8,6 +8,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+#include <mutex>
 #include <string>
 
 #include "../../include/webyiq_q4q8.h"
@@ -38,6 +40,40 @@ int hip_status(hipError_t e, const char* what) {
 }
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Scratch of wq_lm_head_argmax_noalloc: the cross-workgroup argmax slots
+// (keys and tickets, the layout of the caller-provided workspace of
+// wq_lm_head_argmax), one copy per GPU for the life of the process.  Static
+// device memory starts zeroed when the code object loads, and every call
+// leaves it zeroed again.  The host never names the array in a launch: its
+// device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) unsigned char scratch[wq::kArgmaxWorkspaceBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device, with that device current).
+hipError_t scratch_ptr(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return e;
+            if (!p) return hipErrorInvalidSymbol;
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return hipSuccess;
+}
 
 #define REQUIRE_PTR(p)                                                   \
     do {                                                                 \
@@ -371,11 +407,11 @@ int wq_workspace_clear(void* stream, void* workspace, size_t bytes) {
     return hip_status(wq::launch_fill_zero(workspace, bytes, static_cast<hipStream_t>(stream)), fn);
 }
 
-int wq_lm_head_argmax(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t V, int64_t K,
-                      int32_t G, const int8_t* xq, const float* dx, const int32_t* xs, int64_t M,
-                      int32_t GA, const uint32_t* ids, float* logits, uint32_t* tok_out,
-                      void* workspace, size_t workspace_bytes) {
-    const char* fn = "wq_lm_head_argmax";
+namespace {
+
+int lm_head_check(const char* fn, const uint32_t* wq, const uint32_t* ws, int64_t V, int64_t K,
+                  int32_t G, const int8_t* xq, const float* dx, const int32_t* xs, int64_t M,
+                  int32_t GA, float* logits, uint32_t* tok_out) {
     int rc = check_linear(fn, wq, ws, V, K, G, xq, dx, xs, M, GA, WQ_MODE_STORE, logits, false);
     if (rc) return rc;
     rc = check_gemv_shape(fn, M, K);
@@ -383,10 +419,13 @@ int wq_lm_head_argmax(void* stream, const uint32_t* wq, const uint32_t* ws, int6
     REQUIRE_PTR(tok_out);
     REQUIRE_ALIGN(tok_out, 4);
     if (V > (int64_t)0xFFFFFFFEll) return fail(WQ_ESHAPE, "%s: V = %lld out of range", fn, (long long)V);
-    if (!workspace || workspace_bytes < wq::kArgmaxWorkspaceBytes)
-        return fail(WQ_EWORKSPACE, "%s: workspace of %zu bytes required", fn,
-                    (size_t)wq::kArgmaxWorkspaceBytes);
-    REQUIRE_ALIGN(workspace, 8);
+    return WQ_OK;
+}
+
+int lm_head_launch(const char* fn, void* stream, const uint32_t* wq, const uint32_t* ws, int64_t V,
+                   int64_t K, int32_t G, const int8_t* xq, const float* dx, const int32_t* xs,
+                   int64_t M, int32_t GA, const uint32_t* ids, float* logits, uint32_t* tok_out,
+                   void* workspace) {
     auto a = make_args(wq, ws, V, K, G, xq, dx, xs, M, GA, WQ_MODE_STORE, logits, nullptr);
     wq::ArgmaxArgs am{};
     am.ids = ids;
@@ -394,6 +433,39 @@ int wq_lm_head_argmax(void* stream, const uint32_t* wq, const uint32_t* ws, int6
     am.keys = static_cast<unsigned long long*>(workspace);
     am.ticket = reinterpret_cast<unsigned int*>(static_cast<unsigned char*>(workspace) + wq::kArgmaxKeyBytes);
     return hip_status(wq::launch_lm_head_argmax(a, am, static_cast<hipStream_t>(stream)), fn);
+}
+
+}  // namespace
+
+int wq_lm_head_argmax(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t V, int64_t K,
+                      int32_t G, const int8_t* xq, const float* dx, const int32_t* xs, int64_t M,
+                      int32_t GA, const uint32_t* ids, float* logits, uint32_t* tok_out,
+                      void* workspace, size_t workspace_bytes) {
+    const char* fn = "wq_lm_head_argmax";
+    int rc = lm_head_check(fn, wq, ws, V, K, G, xq, dx, xs, M, GA, logits, tok_out);
+    if (rc) return rc;
+    if (!workspace || workspace_bytes < wq::kArgmaxWorkspaceBytes)
+        return fail(WQ_EWORKSPACE, "%s: workspace of %zu bytes required", fn,
+                    (size_t)wq::kArgmaxWorkspaceBytes);
+    REQUIRE_ALIGN(workspace, 8);
+    return lm_head_launch(fn, stream, wq, ws, V, K, G, xq, dx, xs, M, GA, ids, logits, tok_out, workspace);
+}
+
+int wq_lm_head_argmax_noalloc(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t V,
+                              int64_t K, int32_t G, const int8_t* xq, const float* dx,
+                              const int32_t* xs, int64_t M, int32_t GA, const uint32_t* ids,
+                              float* logits, uint32_t* tok_out) {
+    const char* fn = "wq_lm_head_argmax_noalloc";
+    int rc = lm_head_check(fn, wq, ws, V, K, G, xq, dx, xs, M, GA, logits, tok_out);
+    if (rc) return rc;
+    // each of the scratch's kArgmaxSlots slots holds one running key per token
+    if (M > wq::kArgmaxSlotWords)
+        return fail(WQ_ESHAPE, "%s: M = %lld tokens exceeds the %d the scratch holds", fn, (long long)M,
+                    wq::kArgmaxSlotWords);
+    void* p = nullptr;
+    hipError_t e = scratch_ptr(&p);
+    if (e != hipSuccess) return hip_status(e, "wq_lm_head_argmax_noalloc: scratch address");
+    return lm_head_launch(fn, stream, wq, ws, V, K, G, xq, dx, xs, M, GA, ids, logits, tok_out, p);
 }
 
 }  // extern "C"

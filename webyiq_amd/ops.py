@@ -320,6 +320,24 @@ def lm_head_argmax(w: Q4Tensor, a: Acts, ids=None, logits=None, workspace=None, 
     return out
 
 
+def lm_head_argmax_noalloc(w: Q4Tensor, a: Acts, ids=None, logits=None, out=None, stream=None):
+    """lm_head_argmax without a workspace: the reduction runs in the library's
+    own per-device scratch (wq_lm_head_argmax_noalloc).  Calls on one GPU must
+    not overlap."""
+    _check_linear(w, a)
+    d = a.xq.device
+    if ids is not None:
+        _check(ids, "ids", _ID_DTYPES, min_numel=w.rows, device=d)
+    if logits is not None:
+        _check(logits, "logits", torch.float32, shape=(a.M, w.rows), device=d)
+    with _on(stream):
+        out = _tok_out(out, a.M, d)
+        _cuda(w.q, "w.q")
+        _lib.call("wq_lm_head_argmax_noalloc", _cur(), _ptr(w.q), _ptr(w.s), w.rows, w.K, w.G,
+                  _ptr(a.xq), _ptr(a.dx), _ptr(a.xs), a.M, a.GA, _ptr(ids), _ptr(logits), _ptr(out))
+    return out
+
+
 def embed(w: Q4Tensor, tok, out=None, stream=None):
     """int4 embedding lookup (embed.wgsl): x[m] = dequantised row tok[m]."""
     w.check("w")
