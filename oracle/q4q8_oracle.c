@@ -248,14 +248,36 @@ void or_group_acc(const uint32_t* wq, int64_t N, int64_t K, int Ge,
 }
 
 /* Per-group identity of gemv_q4q8.wgsl:6:  sum_i (q s + m)(xq dx) = dx (s A + m X).
- * Canonical fp32 order shared with the kernels: one fmaf chain over the
- * accumulation groups e = 0, 1, ... of the row,
- *   per token (GA = K):  acc = fma(s, A, acc); acc = fma(m, X, acc); a = acc * dx
- *   per 32   (GA = 32):  acc = fma(s*dx_e, A, acc); acc = fma(m*dx_e, X, acc); a = acc */
+ * Canonical fp32 order shared with the kernels (this build's own; the
+ * reference's subgroup reductions cannot be run here):
+ *   per token, G = 128:  four fmaf chains, chain c over the groups e = c, c+4,
+ *                        c+8, ... in index order, each step
+ *                        p_c = fma(s, A, p_c); p_c = fma(m, X, p_c);
+ *                        a = ((p_0 + p_1) + (p_2 + p_3)) * dx
+ *   per token, G = 32:   one chain over e = 0, 1, ...:
+ *                        acc = fma(s, A, acc); acc = fma(m, X, acc); a = acc * dx
+ *   per 32   (GA = 32):  one chain: acc = fma(s*dx_e, A, acc); acc = fma(m*dx_e, X, acc); a = acc */
 static float row_value(const uint32_t* wrow, const uint32_t* srow, int64_t K, int G, int GA,
                        const int8_t* xrow, const float* dxrow, const int32_t* xsrow) {
     int Ge = GA < G ? GA : G;
     int64_t NE = K / Ge;
+    if (GA >= K && G == 128) {
+        float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int64_t e = 0; e < NE; ++e) {
+            int32_t a = 0;
+            for (int i = 0; i < Ge; ++i) {
+                int64_t k = e * Ge + i;
+                a += (int32_t)code(wrow, k) * (int32_t)xrow[k];
+            }
+            uint32_t sw = srow[e];
+            float s = or_f16_to_f32((uint16_t)(sw & 0xFFFFu));
+            float m = or_f16_to_f32((uint16_t)(sw >> 16));
+            int c = (int)(e & 3);
+            p[c] = fmaf(s, (float)a, p[c]);
+            p[c] = fmaf(m, (float)xsrow[e], p[c]);
+        }
+        return ((p[0] + p[1]) + (p[2] + p[3])) * dxrow[0];
+    }
     float acc = 0.0f;
     for (int64_t e = 0; e < NE; ++e) {
         int32_t a = 0;

@@ -401,11 +401,32 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
                 for (int ks = 0; ks < 4; ++ks)
                     af[ks][i] = *reinterpret_cast<const v4i*>(Ab + ra * kBK + 16 * ((4 * h + ks) ^ swz_a(ra)));
             }
+            // with up to 3 columns per wave, every column's packed weight
+            // fragment and scale are read up front (one LDS latency per step
+            // instead of one per column); wider tiles have no registers to spare
+            constexpr bool PRE = TN <= 3;
+            uint4 pb[PRE ? TN : 1][2];
+            float sv[PRE ? TN : 1];
+            if constexpr (PRE) {
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int br = bcol(j);
+                    pb[j][0] = *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * ((2 * h) ^ swz_b(br)));
+                    pb[j][1] = *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * ((2 * h + 1) ^ swz_b(br)));
+                    sv[j] = f16lo(Sb[br]);
+                }
+            }
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 const int br = bcol(j);
-                const uint4 p0 = *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * ((2 * h) ^ swz_b(br)));
-                const uint4 p1 = *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * ((2 * h + 1) ^ swz_b(br)));
+                uint4 p0, p1;
+                if constexpr (PRE) {
+                    p0 = pb[j][0];
+                    p1 = pb[j][1];
+                } else {
+                    p0 = *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * ((2 * h) ^ swz_b(br)));
+                    p1 = *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * ((2 * h + 1) ^ swz_b(br)));
+                }
                 const v4i bf[4] = {expand8(p0.x, p0.y), expand8(p0.z, p0.w), expand8(p1.x, p1.y),
                                    expand8(p1.z, p1.w)};
                 v16i acc[TM];
@@ -415,7 +436,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
                     for (int i = 0; i < TM; ++i)
                         acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks], ks == 0 ? v16i{} : acc[i],
                                                                        0, 0, 0);
-                const float s = f16lo(Sb[br]);
+                const float s = PRE ? sv[PRE ? j : 0] : f16lo(Sb[br]);
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
                     if (DUMP) dump(step, 0, i, br, acc[i]);

@@ -14,9 +14,9 @@
 // result is an exact int32 group sum.  Weight chunks (16 bytes per lane and
 // group) are all issued before the first is used; the int8 activations are
 // staged in LDS once per workgroup.  The fp32 epilogue is the dot4 kernel's
-// -- one chain per (token, row) over the groups in index order,
-// acc = fma(s, A, acc); acc = fma(m, X, acc); y = acc * dx -- so outputs are
-// bit-identical to it and to the oracle.  For K <= 2048 (gemv_mfma_rows_kernel)
+// -- per (token, row) four chains, chain c over the groups i = c (mod 4) in
+// order, p = fma(s, A, p); p = fma(m, X, p); y = ((p0 + p1) + (p2 + p3)) * dx
+// -- so outputs are bit-identical to it and to the oracle.  For K <= 2048 (gemv_mfma_rows_kernel)
 // a wave owns every group of its rows and the chains run in the MFMA result
 // registers; for longer rows the K split meets through LDS.
 #include "argmax_combine.hpp"
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
         const int32_t* ar = acc_lds + ((t * NH + h) * RB + rl) * NGP;
         const float2* sr = sm_lds + (h * RB + rl) * NGP;
         const int32_t* xsr = xs_lds + t * NG;
-        float acc = 0.0f;
+        float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
         int ee = 0;
         if ((NG & 3) == 0) {
             for (; ee < NG; ee += 4) {
@@ -203,22 +203,23 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
                 const float4 x4 = make_float4((float)xi.x, (float)xi.y, (float)xi.z, (float)xi.w);
                 const float4 w01 = *reinterpret_cast<const float4*>(sr + ee);
                 const float4 w23 = *reinterpret_cast<const float4*>(sr + ee + 2);
-                acc = fmaf(w01.x, (float)a4.x, acc);
-                acc = fmaf(w01.y, x4.x, acc);
-                acc = fmaf(w01.z, (float)a4.y, acc);
-                acc = fmaf(w01.w, x4.y, acc);
-                acc = fmaf(w23.x, (float)a4.z, acc);
-                acc = fmaf(w23.y, x4.z, acc);
-                acc = fmaf(w23.z, (float)a4.w, acc);
-                acc = fmaf(w23.w, x4.w, acc);
+                p0 = fmaf(w01.x, (float)a4.x, p0);
+                p0 = fmaf(w01.y, x4.x, p0);
+                p1 = fmaf(w01.z, (float)a4.y, p1);
+                p1 = fmaf(w01.w, x4.y, p1);
+                p2 = fmaf(w23.x, (float)a4.z, p2);
+                p2 = fmaf(w23.y, x4.z, p2);
+                p3 = fmaf(w23.z, (float)a4.w, p3);
+                p3 = fmaf(w23.w, x4.w, p3);
             }
         }
         for (; ee < NG; ++ee) {
             const float2 w = sr[ee];
-            acc = fmaf(w.x, (float)ar[ee], acc);
-            acc = fmaf(w.y, (float)xsr[ee], acc);
+            float& pc = (ee & 3) == 0 ? p0 : (ee & 3) == 1 ? p1 : (ee & 3) == 2 ? p2 : p3;
+            pc = fmaf(w.x, (float)ar[ee], pc);
+            pc = fmaf(w.y, (float)xsr[ee], pc);
         }
-        return acc * dx_lds[t];
+        return ((p0 + p1) + (p2 + p3)) * dx_lds[t];
     };
     if (!ARGMAX) {
         for (int o = tid; o < MT * RB; o += 256) {
@@ -365,11 +366,14 @@ __global__ __launch_bounds__(64 * kRowsWaves) void gemv_mfma_rows_kernel(MfmaGem
         }
         __syncthreads();
         // fp32 chains of (token 4 q + j, row) over the groups in order
-        float acc[NH][4];
+        // four chains per (token, row): chain c over the groups i = c (mod 4)
+        float acc[NH][4][4];
 #pragma unroll
         for (int h = 0; h < NH; ++h)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[h][j] = 0.0f;
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int c4 = 0; c4 < 4; ++c4) acc[h][j][c4] = 0.0f;
 #pragma unroll
         for (int i = 0; i < kMaxGpw; ++i) {
             if (i >= NG) continue;
@@ -379,8 +383,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void gemv_mfma_rows_kernel(MfmaGem
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
-                    acc[h][j] = fmaf(w.x, (float)dres[h][i][j], acc[h][j]);
-                    acc[h][j] = fmaf(w.y, (float)xs_lds[t * NG + i], acc[h][j]);
+                    acc[h][j][i & 3] = fmaf(w.x, (float)dres[h][i][j], acc[h][j][i & 3]);
+                    acc[h][j][i & 3] = fmaf(w.y, (float)xs_lds[t * NG + i], acc[h][j][i & 3]);
                 }
             }
         }
@@ -389,7 +393,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void gemv_mfma_rows_kernel(MfmaGem
         for (int j = 0; j < 4; ++j) {
             const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
 #pragma unroll
-            for (int h = 0; h < NH; ++h) v[h][j] = acc[h][j] * dx_lds[t];
+            for (int h = 0; h < NH; ++h)
+                v[h][j] = ((acc[h][j][0] + acc[h][j][1]) + (acc[h][j][2] + acc[h][j][3])) * dx_lds[t];
         }
         if (a.acc_dump) {  // test hook: the group sums the chains folded
             const int rows_total = NH * (int)N;

@@ -16,9 +16,11 @@
 //
 // Each lane computes its 32-code dot product with 8 v_dot4_i32_i8, a quad of
 // lanes (DPP) completes a 128-group; the exact int32 group sums go to LDS.
-// The fp32 epilogue then runs one fma chain per (token, row) over the groups
-// in index order, the order the CPU oracle restates, so outputs are
-// bit-reproducible (modes 0 and 1) and the fused argmax sees the same logits.
+// The fp32 epilogue then folds each (token, row) in a fixed order the CPU
+// oracle restates -- per-token group-128: four fma chains over the groups
+// e = 0, 1, 2, 3 (mod 4), added ((p0 + p1) + (p2 + p3)); otherwise one chain
+// over the groups in index order -- so outputs are bit-reproducible (modes 0
+// and 1) and the fused argmax sees the same logits.
 #include "argmax_combine.hpp"
 #include "common.hpp"
 #include "launch.hpp"
@@ -304,7 +306,57 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         const float* xsr = xs_lds + t * NE;
         const float* dr = dx_lds + t * NDX;
         float acc = 0.0f;
-        if (PT) {
+        if (PT && G == 128) {
+            // four chains, chain c over the groups e = c (mod 4) in order,
+            // then ((p0 + p1) + (p2 + p3)): a quarter of the dependent fmas
+            float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+            int ee = 0;
+            if ((NE & 3) == 0) {
+                for (; ee + 16 <= NE; ee += 16) {
+                    int4 a4[4];
+                    float4 x4[4], w01[4], w23[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        a4[q] = *reinterpret_cast<const int4*>(ar + ee + 4 * q);
+                        x4[q] = *reinterpret_cast<const float4*>(xsr + ee + 4 * q);
+                        w01[q] = *reinterpret_cast<const float4*>(sr + ee + 4 * q);
+                        w23[q] = *reinterpret_cast<const float4*>(sr + ee + 4 * q + 2);
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        p0 = fmaf(w01[q].x, (float)a4[q].x, p0);
+                        p0 = fmaf(w01[q].y, x4[q].x, p0);
+                        p1 = fmaf(w01[q].z, (float)a4[q].y, p1);
+                        p1 = fmaf(w01[q].w, x4[q].y, p1);
+                        p2 = fmaf(w23[q].x, (float)a4[q].z, p2);
+                        p2 = fmaf(w23[q].y, x4[q].z, p2);
+                        p3 = fmaf(w23[q].z, (float)a4[q].w, p3);
+                        p3 = fmaf(w23[q].w, x4[q].w, p3);
+                    }
+                }
+                for (; ee < NE; ee += 4) {
+                    const int4 a4 = *reinterpret_cast<const int4*>(ar + ee);
+                    const float4 x4 = *reinterpret_cast<const float4*>(xsr + ee);
+                    const float4 w01 = *reinterpret_cast<const float4*>(sr + ee);
+                    const float4 w23 = *reinterpret_cast<const float4*>(sr + ee + 2);
+                    p0 = fmaf(w01.x, (float)a4.x, p0);
+                    p0 = fmaf(w01.y, x4.x, p0);
+                    p1 = fmaf(w01.z, (float)a4.y, p1);
+                    p1 = fmaf(w01.w, x4.y, p1);
+                    p2 = fmaf(w23.x, (float)a4.z, p2);
+                    p2 = fmaf(w23.y, x4.z, p2);
+                    p3 = fmaf(w23.z, (float)a4.w, p3);
+                    p3 = fmaf(w23.w, x4.w, p3);
+                }
+            }
+            for (; ee < NE; ++ee) {
+                const float2 w = sr[ee];
+                float& pc = (ee & 3) == 0 ? p0 : (ee & 3) == 1 ? p1 : (ee & 3) == 2 ? p2 : p3;
+                pc = fmaf(w.x, (float)ar[ee], pc);
+                pc = fmaf(w.y, xsr[ee], pc);
+            }
+            return ((p0 + p1) + (p2 + p3)) * dr[0];
+        } else if (PT) {
             int ee = 0;
             // the (A, X, s, m) operands of a block are read before its fma
             // chain: one LDS round trip per 16 groups (same fma order)
