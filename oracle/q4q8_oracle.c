@@ -250,10 +250,11 @@ void or_group_acc(const uint32_t* wq, int64_t N, int64_t K, int Ge,
 /* Per-group identity of gemv_q4q8.wgsl:6:  sum_i (q s + m)(xq dx) = dx (s A + m X).
  * Canonical fp32 order shared with the kernels (this build's own; the
  * reference's subgroup reductions cannot be run here):
- *   per token, G = 128:  four fmaf chains, chain c over the groups e = c, c+4,
- *                        c+8, ... in index order, each step
- *                        p_c = fma(s, A, p_c); p_c = fma(m, X, p_c);
- *                        a = ((p_0 + p_1) + (p_2 + p_3)) * dx
+ *   per token, G = 128:  per pass of 2048 codes (16 groups), eight chains,
+ *                        chain i over the groups 16p + 2i, 16p + 2i + 1 that
+ *                        exist: c = fma(s, A, c); c = fma(m, X, c) from c = 0;
+ *                        T_p = ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7));
+ *                        the pass sums added left to right; a = total * dx
  *   per token, G = 32:   one chain over e = 0, 1, ...:
  *                        acc = fma(s, A, acc); acc = fma(m, X, acc); a = acc * dx
  *   per 32   (GA = 32):  one chain: acc = fma(s*dx_e, A, acc); acc = fma(m*dx_e, X, acc); a = acc */
@@ -262,21 +263,30 @@ static float row_value(const uint32_t* wrow, const uint32_t* srow, int64_t K, in
     int Ge = GA < G ? GA : G;
     int64_t NE = K / Ge;
     if (GA >= K && G == 128) {
-        float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int64_t e = 0; e < NE; ++e) {
-            int32_t a = 0;
-            for (int i = 0; i < Ge; ++i) {
-                int64_t k = e * Ge + i;
-                a += (int32_t)code(wrow, k) * (int32_t)xrow[k];
+        float total = 0.0f;
+        for (int64_t e0 = 0; e0 < NE; e0 += 16) {
+            float c[8];
+            for (int q = 0; q < 8; ++q) {
+                c[q] = 0.0f;
+                for (int k = 0; k < 2; ++k) {
+                    int64_t e = e0 + 2 * q + k;
+                    if (e >= NE) break;
+                    int32_t a = 0;
+                    for (int i = 0; i < Ge; ++i) {
+                        int64_t kk = e * Ge + i;
+                        a += (int32_t)code(wrow, kk) * (int32_t)xrow[kk];
+                    }
+                    uint32_t sw = srow[e];
+                    float s = or_f16_to_f32((uint16_t)(sw & 0xFFFFu));
+                    float m = or_f16_to_f32((uint16_t)(sw >> 16));
+                    c[q] = fmaf(s, (float)a, c[q]);
+                    c[q] = fmaf(m, (float)xsrow[e], c[q]);
+                }
             }
-            uint32_t sw = srow[e];
-            float s = or_f16_to_f32((uint16_t)(sw & 0xFFFFu));
-            float m = or_f16_to_f32((uint16_t)(sw >> 16));
-            int c = (int)(e & 3);
-            p[c] = fmaf(s, (float)a, p[c]);
-            p[c] = fmaf(m, (float)xsrow[e], p[c]);
+            float t = ((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]));
+            total = e0 == 0 ? t : total + t;
         }
-        return ((p[0] + p[1]) + (p[2] + p[3])) * dxrow[0];
+        return total * dxrow[0];
     }
     float acc = 0.0f;
     for (int64_t e = 0; e < NE; ++e) {

@@ -69,6 +69,8 @@ constexpr int kDppHalfMirror = 0x141;
 constexpr int kDppMirror = 0x140;
 constexpr int kDppBcast15 = 0x142;
 constexpr int kDppBcast31 = 0x143;
+constexpr int kDppRowShr4 = 0x114;  // lane i of a row reads lane i - 4 (0 for i < 4)
+constexpr int kDppRowShr8 = 0x118;  // lane i of a row reads lane i - 8 (0 for i < 8)
 
 template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ int dpp_i(int v) {
@@ -93,6 +95,26 @@ __device__ __forceinline__ float wave_sum_tree(float v) {
     v = v + dpp_f<kDppBcast15, 0xA>(v);  // rows 0, 2 add +0 (unused)
     v = v + dpp_f<kDppBcast31, 0xC>(v);  // row 3: (R2 + R3) + (R0 + R1)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// One pass (16 groups of 128 codes, quad k of 16-lane row r = group 4r + k,
+// every lane of a quad holding its group's s, A, m, X) folded in the
+// canonical per-token order: each pair of groups (2i, 2i + 1) that exists
+// runs the chain c = fma(s, A, c); c = fma(m, X, c) from c = 0 (row_shr:4
+// hands quad 2k's value to quad 2k + 1, which completes the pair); the 8
+// pair values then meet as a pairwise tree, ((p0 + p1) + (p2 + p3)) +
+// ((p4 + p5) + (p6 + p7)) (row_shr:8 pairs a row's two pairs, row_bcast15/31
+// the rows).  Returned to every lane.  c never becomes -0 (each step rounds
+// an exact sum with +0 or a non-zero term to nearest), so a skipped
+// group's pass-through and an empty pair's +0 are the oracle's.
+__device__ __forceinline__ float pass_pairs8(bool act, float s, float A, float m, float X) {
+    float c = act ? fmaf(m, X, fmaf(s, A, 0.0f)) : 0.0f;
+    const float ci = dpp_f<kDppRowShr4>(c);  // quads 1, 3: the pair's first group
+    c = act ? fmaf(m, X, fmaf(s, A, ci)) : ci;
+    c = c + dpp_f<kDppRowShr8>(c);           // lanes 12..15: p(2r + 1) + p(2r)
+    c = c + dpp_f<kDppBcast15, 0xA>(c);      // rows 1, 3: row r + row r - 1
+    c = c + dpp_f<kDppBcast31, 0xC>(c);      // row 3: rows 2, 3 + rows 0, 1
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), 63));
 }
 
 // Sum of squares of one float4 chunk: an fmaf chain in index order.

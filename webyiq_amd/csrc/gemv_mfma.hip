@@ -14,9 +14,10 @@
 // result is an exact int32 group sum.  Weight chunks (16 bytes per lane and
 // group) are all issued before the first is used; the int8 activations are
 // staged in LDS once per workgroup.  The fp32 epilogue is the dot4 kernel's
-// -- per (token, row) four chains, chain c over the groups i = c (mod 4) in
-// order, p = fma(s, A, p); p = fma(m, X, p); y = ((p0 + p1) + (p2 + p3)) * dx
-// -- so outputs are bit-identical to it and to the oracle.  For K <= 2048 (gemv_mfma_rows_kernel)
+// order -- per (token, row) and pass of 16 groups, eight chains
+// c = fma(s, A, c); c = fma(m, X, c) over the pairs of groups (2i, 2i + 1),
+// the pairwise tree over the 8 pair values, the pass sums in order, times
+// dx -- so outputs are bit-identical to it and to the oracle.  For K <= 2048 (gemv_mfma_rows_kernel)
 // a wave owns every group of its rows and the chains run in the MFMA result
 // registers; for longer rows the K split meets through LDS.
 #include "argmax_combine.hpp"
@@ -30,6 +31,12 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kMaxGpw = 16;  // groups per wave
+static_assert(kMaxGpw == 16, "the fold's eight pair chains span the 16 groups of a 2048-code pass");
+
+// The pairwise tree over a pass's 8 pair values.
+__device__ __forceinline__ float tree8(const float (&p)[8]) {
+    return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+}
 // waves per workgroup of the K <= 2048 register-chain kernel
 #ifndef WQ_MFMA_ROWS_WAVES
 #define WQ_MFMA_ROWS_WAVES 4
@@ -194,32 +201,43 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
         const int32_t* ar = acc_lds + ((t * NH + h) * RB + rl) * NGP;
         const float2* sr = sm_lds + (h * RB + rl) * NGP;
         const int32_t* xsr = xs_lds + t * NG;
-        float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
-        int ee = 0;
-        if ((NG & 3) == 0) {
-            for (; ee < NG; ee += 4) {
-                const int4 a4 = *reinterpret_cast<const int4*>(ar + ee);
-                const int4 xi = *reinterpret_cast<const int4*>(xsr + ee);
-                const float4 x4 = make_float4((float)xi.x, (float)xi.y, (float)xi.z, (float)xi.w);
-                const float4 w01 = *reinterpret_cast<const float4*>(sr + ee);
-                const float4 w23 = *reinterpret_cast<const float4*>(sr + ee + 2);
-                p0 = fmaf(w01.x, (float)a4.x, p0);
-                p0 = fmaf(w01.y, x4.x, p0);
-                p1 = fmaf(w01.z, (float)a4.y, p1);
-                p1 = fmaf(w01.w, x4.y, p1);
-                p2 = fmaf(w23.x, (float)a4.z, p2);
-                p2 = fmaf(w23.y, x4.z, p2);
-                p3 = fmaf(w23.z, (float)a4.w, p3);
-                p3 = fmaf(w23.w, x4.w, p3);
+        // per pass of 16 groups a chain per pair of groups (those that
+        // exist), the pairwise tree over the 8 pairs, the pass sums added
+        // in order
+        float total = 0.0f;
+        for (int e0 = 0; e0 < NG; e0 += 16) {
+            float c[8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int ee = e0 + 4 * q;
+                float c0 = 0.0f, c1 = 0.0f;
+                if (ee + 3 < NG && (NG & 3) == 0) {
+                    const int4 a4 = *reinterpret_cast<const int4*>(ar + ee);
+                    const int4 xi = *reinterpret_cast<const int4*>(xsr + ee);
+                    const float4 w01 = *reinterpret_cast<const float4*>(sr + ee);
+                    const float4 w23 = *reinterpret_cast<const float4*>(sr + ee + 2);
+                    c0 = fmaf(w01.y, (float)xi.x, fmaf(w01.x, (float)a4.x, c0));
+                    c0 = fmaf(w01.w, (float)xi.y, fmaf(w01.z, (float)a4.y, c0));
+                    c1 = fmaf(w23.y, (float)xi.z, fmaf(w23.x, (float)a4.z, c1));
+                    c1 = fmaf(w23.w, (float)xi.w, fmaf(w23.z, (float)a4.w, c1));
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const int ek = ee + k;
+                        if (ek < NG) {
+                            const float2 w = sr[ek];
+                            float& cc = k < 2 ? c0 : c1;
+                            cc = fmaf(w.y, (float)xsr[ek], fmaf(w.x, (float)ar[ek], cc));
+                        }
+                    }
+                }
+                c[2 * q] = c0;
+                c[2 * q + 1] = c1;
             }
+            const float tp = tree8(c);
+            total = e0 == 0 ? tp : total + tp;
         }
-        for (; ee < NG; ++ee) {
-            const float2 w = sr[ee];
-            float& pc = (ee & 3) == 0 ? p0 : (ee & 3) == 1 ? p1 : (ee & 3) == 2 ? p2 : p3;
-            pc = fmaf(w.x, (float)ar[ee], pc);
-            pc = fmaf(w.y, (float)xsr[ee], pc);
-        }
-        return ((p0 + p1) + (p2 + p3)) * dx_lds[t];
+        return total * dx_lds[t];
     };
     if (!ARGMAX) {
         for (int o = tid; o < MT * RB; o += 256) {
@@ -365,36 +383,33 @@ __global__ __launch_bounds__(64 * kRowsWaves) void gemv_mfma_rows_kernel(MfmaGem
             }
         }
         __syncthreads();
-        // fp32 chains of (token 4 q + j, row) over the groups in order
-        // four chains per (token, row): chain c over the groups i = c (mod 4)
-        float acc[NH][4][4];
+        // fp32 fold of (token 4 q + j, row): a chain per pair of groups
+        // (those that exist), the pairwise tree over the 8 pairs
+        float v[NH][4];
 #pragma unroll
-        for (int h = 0; h < NH; ++h)
+        for (int h = 0; h < NH; ++h) {
+            float cc[4][8];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int c4 = 0; c4 < 4; ++c4) acc[h][j][c4] = 0.0f;
+                for (int k = 0; k < 8; ++k) cc[j][k] = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kMaxGpw; ++i) {
-            if (i >= NG) continue;
+            for (int i = 0; i < kMaxGpw; ++i) {
+                if (i < NG) {  // uniform
+                    const float2 w = sm_lds[(h * RB + 16 * wave + c) * NGP + i];
 #pragma unroll
-            for (int h = 0; h < NH; ++h) {
-                const float2 w = sm_lds[(h * RB + 16 * wave + c) * NGP + i];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
-                    acc[h][j][i & 3] = fmaf(w.x, (float)dres[h][i][j], acc[h][j][i & 3]);
-                    acc[h][j][i & 3] = fmaf(w.y, (float)xs_lds[t * NG + i], acc[h][j][i & 3]);
+                    for (int j = 0; j < 4; ++j) {
+                        const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
+                        cc[j][i / 2] = fmaf(w.y, (float)xs_lds[t * NG + i],
+                                            fmaf(w.x, (float)dres[h][i][j], cc[j][i / 2]));
+                    }
                 }
             }
-        }
-        float v[NH][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
-#pragma unroll
-            for (int h = 0; h < NH; ++h)
-                v[h][j] = ((acc[h][j][0] + acc[h][j][1]) + (acc[h][j][2] + acc[h][j][3])) * dx_lds[t];
+            for (int j = 0; j < 4; ++j) {
+                const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
+                v[h][j] = tree8(cc[j]) * dx_lds[t];
+            }
         }
         if (a.acc_dump) {  // test hook: the group sums the chains folded
             const int rows_total = NH * (int)N;

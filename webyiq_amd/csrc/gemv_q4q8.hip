@@ -16,11 +16,15 @@
 //
 // Each lane computes its 32-code dot product with 8 v_dot4_i32_i8, a quad of
 // lanes (DPP) completes a 128-group; the exact int32 group sums go to LDS.
-// The fp32 epilogue then folds each (token, row) in a fixed order the CPU
-// oracle restates -- per-token group-128: four fma chains over the groups
-// e = 0, 1, 2, 3 (mod 4), added ((p0 + p1) + (p2 + p3)); otherwise one chain
-// over the groups in index order -- so outputs are bit-reproducible (modes 0
-// and 1) and the fused argmax sees the same logits.
+// The fp32 epilogue folds each (token, row) in a fixed order the CPU oracle
+// restates, so outputs are bit-reproducible (modes 0 and 1) and the fused
+// argmax sees the same logits.  Per-token group-128 (the BASELINE format):
+// per 2048-code pass of 16 groups, eight chains c = fma(s, A, c);
+// c = fma(m, X, c) over the pairs of groups (2i, 2i + 1), the pairwise tree
+// over the 8 pair values, the pass sums added in order -- for one token in
+// registers (DPP moves across the wave's quads, no LDS round trip when a
+// row is one pass), for more through LDS, four lanes per (token, row).  The
+// other formats: one fma chain per (token, row) over the groups in order.
 #include "argmax_combine.hpp"
 #include "common.hpp"
 #include "launch.hpp"
@@ -306,57 +310,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         const float* xsr = xs_lds + t * NE;
         const float* dr = dx_lds + t * NDX;
         float acc = 0.0f;
-        if (PT && G == 128) {
-            // four chains, chain c over the groups e = c (mod 4) in order,
-            // then ((p0 + p1) + (p2 + p3)): a quarter of the dependent fmas
-            float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
-            int ee = 0;
-            if ((NE & 3) == 0) {
-                for (; ee + 16 <= NE; ee += 16) {
-                    int4 a4[4];
-                    float4 x4[4], w01[4], w23[4];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        a4[q] = *reinterpret_cast<const int4*>(ar + ee + 4 * q);
-                        x4[q] = *reinterpret_cast<const float4*>(xsr + ee + 4 * q);
-                        w01[q] = *reinterpret_cast<const float4*>(sr + ee + 4 * q);
-                        w23[q] = *reinterpret_cast<const float4*>(sr + ee + 4 * q + 2);
-                    }
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        p0 = fmaf(w01[q].x, (float)a4[q].x, p0);
-                        p0 = fmaf(w01[q].y, x4[q].x, p0);
-                        p1 = fmaf(w01[q].z, (float)a4[q].y, p1);
-                        p1 = fmaf(w01[q].w, x4[q].y, p1);
-                        p2 = fmaf(w23[q].x, (float)a4[q].z, p2);
-                        p2 = fmaf(w23[q].y, x4[q].z, p2);
-                        p3 = fmaf(w23[q].z, (float)a4[q].w, p3);
-                        p3 = fmaf(w23[q].w, x4[q].w, p3);
-                    }
-                }
-                for (; ee < NE; ee += 4) {
-                    const int4 a4 = *reinterpret_cast<const int4*>(ar + ee);
-                    const float4 x4 = *reinterpret_cast<const float4*>(xsr + ee);
-                    const float4 w01 = *reinterpret_cast<const float4*>(sr + ee);
-                    const float4 w23 = *reinterpret_cast<const float4*>(sr + ee + 2);
-                    p0 = fmaf(w01.x, (float)a4.x, p0);
-                    p0 = fmaf(w01.y, x4.x, p0);
-                    p1 = fmaf(w01.z, (float)a4.y, p1);
-                    p1 = fmaf(w01.w, x4.y, p1);
-                    p2 = fmaf(w23.x, (float)a4.z, p2);
-                    p2 = fmaf(w23.y, x4.z, p2);
-                    p3 = fmaf(w23.z, (float)a4.w, p3);
-                    p3 = fmaf(w23.w, x4.w, p3);
-                }
-            }
-            for (; ee < NE; ++ee) {
-                const float2 w = sr[ee];
-                float& pc = (ee & 3) == 0 ? p0 : (ee & 3) == 1 ? p1 : (ee & 3) == 2 ? p2 : p3;
-                pc = fmaf(w.x, (float)ar[ee], pc);
-                pc = fmaf(w.y, xsr[ee], pc);
-            }
-            return ((p0 + p1) + (p2 + p3)) * dr[0];
-        } else if (PT) {
+        if (PT) {
             int ee = 0;
             // the (A, X, s, m) operands of a block are read before its fma
             // chain: one LDS round trip per 16 groups (same fma order)
@@ -441,6 +395,119 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
             *yo = silu_mul(v, chain(t, 1, rl));
         }
     };
+    if constexpr (PT && G == 128 && MT == 1) {
+        // Per-token group-128 epilogue in registers (one token: few outputs
+        // per workgroup, so latency matters more than lane occupancy).
+        // After quad_sum every lane of a quad holds its group's exact sum A,
+        // and pass_pairs8 folds the pass's 16 groups in the canonical order
+        // (a chain per pair of groups, the pairwise tree over the pairs).
+        // A row of one pass (K <= 2048) is complete in its wave; with several
+        // passes the wave sums meet through LDS and are added in pass order.
+        const bool lead = kact && (lane & 3) == 0;
+        const int rows_total = NH * (int)N;
+        float vals[NH][IPW][MT];
+#pragma unroll
+        for (int s = 0; s < IPW; ++s) {
+            const int64_t row = r0 + slot + p.nslots * s;
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const float ws_s = f16lo(sv[h][s]), ws_m = f16hi(sv[h][s]);
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    const int d = quad_sum(dot32(wv[h][s], xa[t], xb[t]));
+                    if (a.acc_dump && lead && t < a.M && row < N)  // test hook: the exact group sums
+                        a.acc_dump[((int64_t)t * rows_total + h * N + row) * NE + e] = d;
+                    vals[h][s][t] = pass_pairs8(kact, ws_s, (float)d, ws_m, (float)xsv[t]);
+                }
+            }
+        }
+        unsigned long long* keys = lds_align<8, unsigned long long>(smem, dx_lds + (size_t)MT * NDX);
+        // y (or the argmax key) of (token t, local row rl) from the row sums
+        auto emit = [&](int t, int rl, float v0, float v1, float d) {
+            const int64_t row = r0 + rl;
+            const bool ok = t < a.M && row < N;
+            if constexpr (ARGMAX) {
+                unsigned long long key = 0;
+                if (ok) {
+                    const float v = v0 * d;
+                    if (a.y) a.y[(int64_t)t * N + row] = v;
+                    if (v > -3.0e38f) key = argmax_key(v, (uint32_t)row);
+                }
+                keys[t * RB + rl] = key;
+            } else if (ok) {
+                float* yo = a.y + (int64_t)t * N + row;
+                const float v = v0 * d;
+                if (MODE == 0) {
+                    *yo = v;
+                } else if (MODE == 1) {
+                    *yo = *yo + v;
+                } else {
+                    *yo = silu_mul(v, v1 * d);
+                }
+            }
+        };
+        static_assert(IPW * MT <= 64, "one lane per (row, token)");
+        if (p.J == 1) {
+            // lane s * MT + t of the wave emits (token t, its row s)
+            float v0 = 0.0f, v1 = 0.0f, dsel = 0.0f;
+            int tsel = -1, rsel = 0;
+#pragma unroll
+            for (int s = 0; s < IPW; ++s)
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+                    if (lane == s * MT + t) {
+                        v0 = vals[0][s][t];
+                        v1 = vals[NH - 1][s][t];
+                        dsel = dxv[t];
+                        tsel = t;
+                        rsel = slot + p.nslots * s;
+                    }
+            if (tsel >= 0) emit(tsel, rsel, v0, v1, dsel);
+        } else {
+            // pass sums [t][h][rl][pass] -> LDS, then each (token, row) adds
+            // its passes left to right
+            float* part = reinterpret_cast<float*>(acc_lds);
+            const int J = p.J;
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                float v = 0.0f;
+                int idx = -1;
+#pragma unroll
+                for (int s = 0; s < IPW; ++s)
+#pragma unroll
+                    for (int t = 0; t < MT; ++t)
+                        if (lane == s * MT + t) {
+                            v = vals[h][s][t];
+                            idx = ((t * NH + h) * RB + slot + p.nslots * s) * J + j;
+                        }
+                if (idx >= 0) part[idx] = v;
+            }
+            if (tid == 0) {
+#pragma unroll
+                for (int t = 0; t < MT; ++t) dx_lds[t] = dxv[t];
+            }
+            __syncthreads();
+            for (int o = tid; o < MT * RB; o += nthreads) {
+                const int t = o / RB, rl = o - t * RB;
+                float v[NH];
+#pragma unroll
+                for (int h = 0; h < NH; ++h) {
+                    const float* pp = part + ((t * NH + h) * RB + rl) * J;
+                    float tot = pp[0];
+                    for (int jj = 1; jj < J; ++jj) tot = tot + pp[jj];
+                    v[h] = tot;
+                }
+                emit(t, rl, v[0], v[NH - 1], dx_lds[t]);
+            }
+        }
+        if constexpr (ARGMAX) {
+            __syncthreads();
+            const unsigned long long best = block_best<MT>(keys, RB, (int)a.M);
+            argmax_combine<MT>(p.am, (int)a.M, p.nblocks, best);
+        }
+        return;
+    }
+
     // 2. activation sums / scales and weight (s, m) -> LDS
     if (slot == 0 && kact && (lane % LPG) == 0) {
 #pragma unroll
@@ -485,6 +552,85 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
                 a.acc_dump[((int64_t)t * rows_total + h * N + row) * NE + ee] =
                     acc_lds[((t * NH + h) * RB + rl) * NEP + ee];
         }
+    }
+
+    if constexpr (PT && G == 128) {
+        // Per-token group-128, several tokens: four lanes per (token, row).
+        // Per pass, lane q runs the pair chains c = fma(s, A, c);
+        // c = fma(m, X, c) from 0 over groups (4q, 4q + 1) and (4q + 2,
+        // 4q + 3) (those that exist) and adds the two; two quad moves
+        // complete the pairwise tree over the 8 pairs; the pass sums are
+        // added in order.  The register epilogue's order.
+        unsigned long long* keys = lds_align<8, unsigned long long>(smem, dx_lds + (size_t)MT * NDX);
+        const bool vec = (NE & 3) == 0;
+        for (int o = tid; o < 4 * MT * RB; o += nthreads) {
+            const int q = o & 3, oo = o >> 2;
+            const int t = oo / RB, rl = oo - t * RB;
+            const float* xsr = xs_lds + t * NE;
+            float tot[NH];
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const int32_t* ar = acc_lds + ((t * NH + h) * RB + rl) * NEP;
+                const float2* sr = sm_lds + (h * RB + rl) * NGS;
+                float total = 0.0f;
+                for (int e0 = 0; e0 < NE; e0 += 16) {
+                    const int eb = e0 + 4 * q;
+                    float c0 = 0.0f, c1 = 0.0f;
+                    if (vec && eb < NE) {
+                        const int4 a4 = *reinterpret_cast<const int4*>(ar + eb);
+                        const float4 x4 = *reinterpret_cast<const float4*>(xsr + eb);
+                        const float4 w01 = *reinterpret_cast<const float4*>(sr + eb);
+                        const float4 w23 = *reinterpret_cast<const float4*>(sr + eb + 2);
+                        c0 = fmaf(w01.y, x4.x, fmaf(w01.x, (float)a4.x, c0));
+                        c0 = fmaf(w01.w, x4.y, fmaf(w01.z, (float)a4.y, c0));
+                        c1 = fmaf(w23.y, x4.z, fmaf(w23.x, (float)a4.z, c1));
+                        c1 = fmaf(w23.w, x4.w, fmaf(w23.z, (float)a4.w, c1));
+                    } else if (!vec) {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (eb + k < NE) {
+                                const float2 w = sr[eb + k];
+                                float& c = k < 2 ? c0 : c1;
+                                c = fmaf(w.y, xsr[eb + k], fmaf(w.x, (float)ar[eb + k], c));
+                            }
+                    }
+                    float v = c0 + c1;
+                    v = v + dpp_f<kDppXor1>(v);
+                    v = v + dpp_f<kDppXor2>(v);
+                    total = e0 == 0 ? v : total + v;
+                }
+                tot[h] = total;
+            }
+            if (q != 0) continue;
+            const int64_t row = r0 + rl;
+            const bool ok = t < a.M && row < N;
+            const float d = dx_lds[t];
+            if constexpr (ARGMAX) {
+                unsigned long long key = 0;
+                if (ok) {
+                    const float v = tot[0] * d;
+                    if (a.y) a.y[(int64_t)t * N + row] = v;
+                    if (v > -3.0e38f) key = argmax_key(v, (uint32_t)row);
+                }
+                keys[t * RB + rl] = key;
+            } else if (ok) {
+                float* yo = a.y + (int64_t)t * N + row;
+                const float v = tot[0] * d;
+                if (MODE == 0) {
+                    *yo = v;
+                } else if (MODE == 1) {
+                    *yo = *yo + v;
+                } else {
+                    *yo = silu_mul(v, tot[NH - 1] * d);
+                }
+            }
+        }
+        if constexpr (ARGMAX) {
+            __syncthreads();
+            const unsigned long long best = block_best<MT>(keys, RB, (int)a.M);
+            argmax_combine<MT>(p.am, (int)a.M, p.nblocks, best);
+        }
+        return;
     }
 
     if (!ARGMAX) {
