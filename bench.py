@@ -56,6 +56,9 @@ def parse():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-config lines (decode MLP, verify shapes, lm_head)")
     ap.add_argument("--cpu-seconds", type=float, default=24.0)
+    ap.add_argument("--floor", action="store_true",
+                    help="also time the no-arithmetic kernels of bench_floor.hip on the GEMV's grid "
+                         "and weight copies, alternating with the GEMV (per-launch floors)")
     ap.add_argument("--calib-mib", type=int, default=0,
                     help="after the timed region, copy a buffer of this many MiB 8 times "
                          "(the known-size kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -190,6 +193,9 @@ def main():
         "parity": {"gemv_vs_oracle_bit_exact": parity},
     }
 
+    if args.floor:
+        out["floor"] = bench_floor(torch, launches, qs, ss, N)
+
     if args.calib_mib > 0:
         nb = args.calib_mib << 20
         src = torch.empty(nb // 4, dtype=torch.float32, device=dev).fill_(1.0)
@@ -210,6 +216,42 @@ def main():
         out["cpu_baseline"] = cpu_baseline(torch, ref, wq, ws, K, G, x, nbytes, args.cpu_seconds)
 
     print(json.dumps(out), flush=True)
+
+
+def bench_floor(torch, gemv_launches, qs, ss, N):
+    """Per-launch graph-replay time of bench_floor.hip's kernels (empty; read
+    the weight rows and scale words; read and store one word per row) on the
+    GEMV's grid and weight copies, alternating with the GEMV itself over three
+    rounds (medians, us)."""
+    F = ctypes.CDLL(os.path.join(HERE, "bench_floor.so"))
+    F.floor_launch.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                               ctypes.c_int]
+    F.floor_launch.restype = ctypes.c_int
+    out = torch.zeros(N, dtype=torch.int32, device="cuda")
+    P = ctypes.c_void_p
+
+    class Floor:
+        def __init__(self, kind, i):
+            self.args = (kind, P(qs[i].data_ptr()), P(ss[i].data_ptr()), P(out.data_ptr()), N)
+
+        def __call__(self, stream):
+            rc = F.floor_launch(stream, *self.args)
+            if rc != 0:
+                raise RuntimeError(f"floor launch failed [{rc}]")
+
+    R = len(qs)
+    sets = {"empty": [Floor(0, i) for i in range(R)], "read": [Floor(1, i) for i in range(R)],
+            "read_store": [Floor(2, i) for i in range(R)], "gemv": gemv_launches}
+    times = {k: [] for k in sets}
+    for k, lns in sets.items():
+        graph_time(torch, lns, 10)
+    for _ in range(3):
+        for k, lns in sets.items():
+            times[k].append(graph_time(torch, lns, 20) * 1e6)
+    res = {f"{k}_us": round(float(np.median(v)), 3) for k, v in times.items()}
+    res["grid"] = "256 workgroups x 4 waves, 6 rows per wave (the GEMV's plan at M=1, K=2048, N=6144)"
+    res["bytes_read"] = int(N * (1024 + 64))
+    return res
 
 
 def bench_gemm(torch, lib, ops, orc, ref, args):

@@ -177,6 +177,10 @@ GEMV_CASES = [
     (8, 16384, 512, 128, None, 1),
     (8, 8192, 16384, 128, None, 0),
     (1, 16384, 6144, 32, 32, 0),
+    # three rows per wave: the plan for 2 x 768 < N / 4 <= 3 x 768 (K <= 2048)
+    (1, 2048, 8192, 128, None, 0),
+    (2, 2048, 8192, 128, None, 2),
+    (8, 1536, 7000, 128, None, 1),   # partial pass, ragged last block
 ]
 
 

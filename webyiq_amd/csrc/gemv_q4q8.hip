@@ -667,10 +667,13 @@ struct Plan {
     unsigned grid;
 };
 
+// Grid target: 3 workgroups per CU (256 CUs), i.e. three waves per SIMD,
+// whose loads and register epilogues overlap one another.
 #ifndef WQ_GEMV_TARGET_WGS
-#define WQ_GEMV_TARGET_WGS 256
+#define WQ_GEMV_TARGET_WGS 768
 #endif
-constexpr int64_t kGemvTargetWgs = WQ_GEMV_TARGET_WGS;  // MI355X: 256 CUs
+constexpr int64_t kGemvTargetWgs = WQ_GEMV_TARGET_WGS;
+constexpr int64_t kGemvCus = 256;
 
 int round_tokens(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
@@ -687,16 +690,20 @@ Plan make_plan(const LinearArgs& a, bool argmax, bool qin = false) {
     p.NG = (int)(a.K / a.G);
     const int nh = a.mode == 2 ? 2 : 1;
     // rows per wave: the fewest loads per lane that still keep the grid within
-    // kGemvTargetWgs workgroups (every CU busy, all loads issued up front)
+    // the target (all loads issued up front).  With the fused quantiser every
+    // workgroup re-quantises the whole input (MT x K floats from L2), so it
+    // keeps one workgroup per CU per weight half (measured best for the
+    // decode layer's four fused shapes at 1 and 2 tokens).  One row per wave
+    // only where two would leave CUs idle: a wave's second row hides the
+    // first one's arithmetic.
     int ipw = 8;
-    static const int choices[] = {1, 2, 4, 6, 8};
-    // (gate + up pairs and 8-token launches carry twice the epilogue work per
-    // row: 1.5x the workgroups measured faster for them)
-    const int64_t target = (a.mode == 2 || p.MT == 8) ? kGemvTargetWgs * 3 / 2 : kGemvTargetWgs;
+    static const int choices[] = {1, 2, 3, 4, 6, 8};
+    const int64_t target = qin ? kGemvCus * nh : kGemvTargetWgs;
+    auto grid_of = [&](int c) { return (a.N + (int64_t)p.nslots * c - 1) / ((int64_t)p.nslots * c); };
     for (int c : choices) {
-        int64_t rb = (int64_t)p.nslots * c;
-        if ((a.N + rb - 1) / rb <= target) { ipw = c; break; }
+        if (grid_of(c) <= target) { ipw = c; break; }
     }
+    if (ipw == 1 && grid_of(2) >= kGemvCus) ipw = 2;
     // LDS budget: 64 KiB per workgroup
     auto lds_of = [&](int ipw_) {
         size_t rb = (size_t)p.nslots * ipw_;
@@ -713,7 +720,7 @@ Plan make_plan(const LinearArgs& a, bool argmax, bool qin = false) {
         return nh * ipw_ * 4 + 8 * p.MT + (qin ? 4 * (8 / p.nslots) * (p.MT + 1) : 0);
     };
     while (ipw > 1 && (lds_of(ipw) > 65536 || regs_of(ipw) > 96))
-        ipw = ipw == 8 ? 6 : ipw == 6 ? 4 : ipw / 2;
+        ipw = ipw == 8 ? 6 : ipw == 6 ? 4 : ipw - 1;
     p.IPW = ipw;
     p.RB = p.nslots * ipw;
     p.lds = lds_of(ipw);
@@ -727,6 +734,7 @@ hipError_t launch_ipw(const Plan& pl, const GemvParams& gp, hipStream_t s) {
     switch (pl.IPW) {
         case 1: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 1, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
         case 2: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 2, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
+        case 3: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 3, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
         case 4: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 4, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
         case 6: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 6, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
         default: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 8, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
