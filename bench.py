@@ -249,7 +249,7 @@ def bench_floor(torch, gemv_launches, qs, ss, N):
         for k, lns in sets.items():
             times[k].append(graph_time(torch, lns, 20) * 1e6)
     res = {f"{k}_us": round(float(np.median(v)), 3) for k, v in times.items()}
-    res["grid"] = "256 workgroups x 4 waves, 6 rows per wave (the GEMV's plan at M=1, K=2048, N=6144)"
+    res["grid"] = "768 workgroups x 4 waves, 2 rows per wave (the GEMV's plan at M=1, K=2048, N=6144)"
     res["bytes_read"] = int(N * (1024 + 64))
     return res
 

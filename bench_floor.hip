@@ -1,6 +1,6 @@
 // Per-launch floors for the decode GEMV's launch shape (bench.py --floor):
-// kernels on the GEMV's grid for M = 1, K = 2048, N = 6144 (256 workgroups
-// of 4 waves, 6 rows per wave) that do none of its arithmetic.
+// kernels on the GEMV's grid for M = 1, K = 2048, N = 6144 (768 workgroups
+// of 4 waves, 2 rows per wave) that do none of its arithmetic.
 //   empty      -- no loads, no stores: the launch and drain cost alone;
 //   read       -- every weight row (1 KiB, one 16-byte streamed load per
 //                 lane) and its scale words (each lane its group's word),
@@ -16,7 +16,7 @@
 
 namespace {
 
-constexpr int kIpw = 6;      // rows per wave
+constexpr int kIpw = 2;      // rows per wave
 constexpr int kSlots = 4;    // waves per workgroup
 constexpr int kRowU4 = 64;   // 16-byte chunks per 1 KiB row
 constexpr int kRowWs = 16;   // scale words per row (K / 128)
