@@ -33,83 +33,117 @@ __device__ __forceinline__ unsigned long long block_best(const unsigned long lon
     return tid < MT && tid < M ? tok_best[tid] : 0ull;
 }
 
-// Every workgroup calls this once with its best key for token tid in
-// threads tid < M (0 elsewhere).  Keys and tickets live in kArgmaxSlots
-// cache lines; the last workgroup of each slot takes a top ticket; the last
-// of those reduces the slots, writes the token (mapped through ids when set)
-// and clears the workspace for the next call.
+// Spin limit of the final workgroup's wait for the others' tickets (each poll
+// is one device-coherent load plus a short sleep; the limit is ~0.5 s, far
+// beyond any launch, so the wait ends even if a ticket never came).
+constexpr unsigned kArgmaxSpinLimit = 1u << 22;
+
+// Every workgroup calls this once, as its last action, with its best key for
+// token tid in threads tid < M (0 elsewhere).  Keys live in kArgmaxSlots
+// cache lines (workgroup b updates slot b % kArgmaxSlots) and so do the
+// tickets.  Every workgroup but the last one (the highest index, dispatched
+// last) merges its keys, takes a ticket in its slot and ends: its waves
+// past the first leave at once, the first waits for one atomic.  The last
+// workgroup merges its own keys, waits until every slot counts all of its
+// other workgroups, then reduces the slots, writes the token (mapped through
+// ids when set) and clears the workspace for the next call.
 //
 // Ordering without release fences.  A release fence at agent scope writes
 // back the whole L2 of the workgroup's XCD (the 8 XCDs' L2s are not coherent
 // with one another); one per workgroup cost 225 us on the 151,936-row head.
 // The combine instead orders its accesses by completion:
 //  1. Every access to the workspace is an agent-scope atomic (atomicMax and
-//     atomicAdd on device memory, and __hip_atomic_load/store with
+//     fetch-add on device memory, and __hip_atomic_load/store with
 //     __HIP_MEMORY_SCOPE_AGENT).  gfx950 performs these at the device's
 //     coherence point, past the XCD-local L2, not in a per-XCD copy.
 //  2. A returning atomic delivers its value only after it has been performed
-//     there.  The keys' atomicMax results are consumed (the empty asm below)
-//     before the barrier, so thread 0's ticket atomicAdd is issued only after
-//     every key update of its workgroup has been performed.
-//  3. The ticket counts are a total order on each counter.  The workgroup
-//     that reads in_slot - 1 from its slot's counter issued its top-counter
-//     atomicAdd after every other workgroup of the slot had performed its
-//     ticket, hence (by 2) its keys; the same holds one level up for the
-//     workgroup that reads used - 1 from the top counter.
-//  4. That last workgroup then reads the keys with agent-scope atomic loads,
-//     issued after its own top ticket returned, so each load is performed
-//     after every key update, at the same coherence point.
+//     there.  A workgroup's key atomicMax results are consumed (the empty asm
+//     below; the wave waits for all of its lanes) before its first lane
+//     issues the ticket, so each ticket is performed after its workgroup's
+//     key updates have been performed.
+//  3. The last workgroup reads each slot's ticket count with agent-scope
+//     loads until it equals the number of other workgroups of that slot:
+//     every ticket, hence (by 2) every key update, has then been performed.
+//  4. It then reads the keys with agent-scope atomic loads issued after
+//     those polls returned, so each load is performed after every key update,
+//     at the same coherence point.
 // The HIP memory model guarantees visibility only through release/acquire
 // pairs, so points 1, 2 and 4 rest on this hardware's completion order rather
 // than on the language model.  The last workgroup adds an agent-scope
-// acquire fence before its loads (one L2 invalidate on one XCD, not
-// measurable at these sizes), so no stale line of its XCD's L2 can be read
-// even if a key load were served from the L2.
+// acquire fence before its loads (one L2 invalidate on one XCD; measured
+// 0.3-0.4 us per call on the lm_head shapes), so no stale line of its XCD's
+// L2 can be read even if a key load were served from the L2.
+//
+// Cost: the combine adds 2.5-4 us per call on the lm_head shapes, almost all
+// of it after the last stream ends (the last tickets landing, the final
+// workgroup's loads and stores: device-coherent round trips of ~0.3 us idle,
+// longer while the stream drains).
+//
+// Progress: the last workgroup waits only for workgroups of lower index.
+// Workgroups are dispatched in index order, so each of those has been
+// dispatched to some CU when the last one runs; none waits for anything, so
+// each finishes.  The wait is bounded all the same (kArgmaxSpinLimit); if it
+// ran out, the tokens would be written as 0xFFFFFFFF.
 template <int MT>
 __device__ __forceinline__ void argmax_combine(const ArgmaxArgs& am, int M, int nblocks, unsigned long long best) {
-    __shared__ unsigned int last_block;
-    __shared__ unsigned long long slot_keys[kArgmaxSlots * MT];
     const int tid = threadIdx.x, nthreads = blockDim.x;
     const int kslot = (int)(blockIdx.x % kArgmaxSlots);
+    const bool final_block = (int)blockIdx.x == nblocks - 1;
+    if (!final_block && tid >= 64) return;  // only the first wave takes part
     if (tid < MT && tid < M) {
         const unsigned long long old = atomicMax(am.keys + kslot * kArgmaxSlotWords + tid, best);
         asm volatile("" ::"v"(old));  // the returned value: this atomic has been performed
     }
-    __syncthreads();
+    if (!final_block) {
+        if (tid == 0)
+            __hip_atomic_fetch_add(am.ticket + kslot * kArgmaxSlotWords * 2, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+
+    __shared__ unsigned long long slot_keys[kArgmaxSlots * MT];
+    __shared__ unsigned int timed_out;
     const int used = nblocks < kArgmaxSlots ? nblocks : kArgmaxSlots;
-    if (tid == 0) {
-        const unsigned in_slot = (unsigned)((nblocks - kslot + kArgmaxSlots - 1) / kArgmaxSlots);
-        unsigned int done = atomicAdd(am.ticket + kslot * kArgmaxSlotWords * 2, 1u);
-        bool last = false;
-        if (done == in_slot - 1) {
-            unsigned int top = atomicAdd(am.ticket + kArgmaxSlots * kArgmaxSlotWords * 2, 1u);
-            last = top == (unsigned)used - 1;
+    if (tid < 64) {
+        // lane l polls slot l: it expects the other workgroups of that slot
+        const int sl = tid;
+        unsigned want = 0;
+        if (sl < used) {
+            want = (unsigned)((nblocks - sl + kArgmaxSlots - 1) / kArgmaxSlots);
+            if (sl == kslot) want -= 1;  // this workgroup takes no ticket
         }
-        last_block = last;
+        unsigned spins = 0;
+        bool done = false;
+        while (true) {
+            const unsigned have = sl < used ? __hip_atomic_load(am.ticket + sl * kArgmaxSlotWords * 2,
+                                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                            : 0u;
+            done = __all(have >= want);
+            if (done || ++spins >= kArgmaxSpinLimit) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (tid == 0) timed_out = done ? 0u : 1u;
     }
     __syncthreads();
-    if (last_block) {
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        // every slot key read at once (independent device-coherent loads),
-        // then reduced in LDS
-        for (int o = tid; o < used * MT; o += nthreads)
-            slot_keys[o] = __hip_atomic_load(am.keys + (o / MT) * kArgmaxSlotWords + (o % MT), __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        if (tid < M) {
-            unsigned long long k = 0;
-            for (int sl = 0; sl < used; ++sl) k = slot_keys[sl * MT + tid] > k ? slot_keys[sl * MT + tid] : k;
-            uint32_t idx = k ? 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull) : 0u;
-            am.tok_out[tid] = am.ids ? am.ids[idx] : idx;
-        }
-        __syncthreads();
-        for (int o = tid; o < used * MT; o += nthreads)
-            __hip_atomic_store(am.keys + (o / MT) * kArgmaxSlotWords + (o % MT), 0ull, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        for (int o = tid; o <= used; o += nthreads)
-            __hip_atomic_store(am.ticket + (o < used ? o * kArgmaxSlotWords * 2 : kArgmaxSlots * kArgmaxSlotWords * 2),
-                               0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // every slot key read at once (independent device-coherent loads), then
+    // reduced in LDS
+    for (int o = tid; o < used * MT; o += nthreads)
+        slot_keys[o] = __hip_atomic_load(am.keys + (o / MT) * kArgmaxSlotWords + (o % MT), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (tid < M) {
+        unsigned long long k = 0;
+        for (int sl = 0; sl < used; ++sl) k = slot_keys[sl * MT + tid] > k ? slot_keys[sl * MT + tid] : k;
+        uint32_t idx = k ? 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull) : 0u;
+        am.tok_out[tid] = timed_out ? 0xFFFFFFFFu : am.ids ? am.ids[idx] : idx;
     }
+    __syncthreads();
+    for (int o = tid; o < used * MT; o += nthreads)
+        __hip_atomic_store(am.keys + (o / MT) * kArgmaxSlotWords + (o % MT), 0ull, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    for (int o = tid; o < used; o += nthreads)
+        __hip_atomic_store(am.ticket + o * kArgmaxSlotWords * 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace wq

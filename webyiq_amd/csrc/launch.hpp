@@ -37,7 +37,7 @@ struct ArgmaxArgs {
     const uint32_t* ids;  // nullable id map (draft vocabulary)
     uint32_t* tok_out;    // [M]
     unsigned long long* keys;  // workspace: [kArgmaxSlots][8] running (value, index) keys
-    unsigned int* ticket;      // workspace: [kArgmaxSlots] slot counters + 1 top counter, one line each
+    unsigned int* ticket;      // workspace: [kArgmaxSlots] slot ticket counters (+ a spare line), one line each
 };
 
 // Input of a GEMV that quantises its own activations (per token).
@@ -123,7 +123,7 @@ constexpr int kGemvPassK = 2048;
 // Largest token count of the decode GEMV (the M <= 8 speculative-verify case).
 constexpr int kGemvMaxTokens = 8;
 // Workspace of the fused lm_head argmax: kArgmaxSlots cache lines of 8 keys,
-// then kArgmaxSlots + 1 lines holding one counter each.
+// then kArgmaxSlots lines holding one ticket counter each and a spare line.
 constexpr int kArgmaxSlots = 64;
 constexpr int kArgmaxSlotWords = 8;  // 64-bit words per 64-byte line
 constexpr size_t kArgmaxKeyBytes = (size_t)kArgmaxSlots * kArgmaxSlotWords * 8;
