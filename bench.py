@@ -263,7 +263,7 @@ def bench_gemm(torch, lib, ops, orc, ref, args):
         rng = np.random.default_rng(args.seed + K)
         wq, ws = ref.make_weight(rng, N, K, 128)
         x = ref.make_activations(rng, M, K)
-        copies = 8  # 8 x 6.3 MB weights + outputs cycle well past the MALL with y
+        copies = 16  # 16 x (6.3 MB weights + 25.2 MB outputs) = 504 MB, twice the MALL
         q = [torch.from_numpy(wq.view(np.int32)).cuda() for _ in range(copies)]
         s = [torch.from_numpy(ws.view(np.int32)).cuda() for _ in range(copies)]
         a = ops.quant(torch.from_numpy(x).cuda(), G=128)
@@ -309,8 +309,9 @@ def rand_weights(torch, rows, K, G, copies):
     return [(q, s)] + [(q.clone(), s.clone()) for _ in range(copies - 1)]
 
 
-def copies_for(nbytes, budget=512 << 20, cap=64):
-    """Enough weight copies that one rotation exceeds the 256 MB MALL."""
+def copies_for(nbytes, budget=512 << 20, cap=1024):
+    """Enough weight copies that one rotation exceeds the 256 MB MALL
+    (512 MB: the smallest verify shape, N = 512, takes ~940 copies)."""
     return max(2, min(cap, -(-budget // nbytes)))
 
 
@@ -397,7 +398,7 @@ def bench_configs(torch, lib, ops):
     wsp = ops.lm_head_workspace()
     for V in (151936, 32768):
         nbw = V * 2048 // 2 + 4 * V * 2048 // G
-        R = copies_for(nbw, budget=512 << 20, cap=8)
+        R = copies_for(nbw, budget=512 << 20, cap=16)
         ws = rand_weights(torch, V, 2048, G, R)
         for M in (1, 8):
             a = acts(M, 2048)
