@@ -83,7 +83,9 @@ constexpr unsigned kArgmaxSpinLimit = 1u << 22;
 // Workgroups are dispatched in index order, so each of those has been
 // dispatched to some CU when the last one runs; none waits for anything, so
 // each finishes.  The wait is bounded all the same (kArgmaxSpinLimit); if it
-// ran out, the tokens would be written as 0xFFFFFFFF.
+// ran out, the tokens would be written as 0xFFFFFFFF, and tickets landing
+// after the clear would leave the workspace non-zero (wq_workspace_clear
+// before reusing it).
 template <int MT>
 __device__ __forceinline__ void argmax_combine(const ArgmaxArgs& am, int M, int nblocks, unsigned long long best) {
     const int tid = threadIdx.x, nthreads = blockDim.x;
