@@ -27,6 +27,8 @@
 // scales) fold both terms on the VALU in the GEMV's order, bit for bit.  Tiles
 // are assigned XCD by XCD so that the workgroups sharing a weight tile share
 // one L2.
+#include <type_traits>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -494,7 +496,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
         }
     };
 
-    if (KS == 1) {
+    if constexpr (KS == 1) {
         // step s: load step s + NST - 1 into stage (s - 1) % NST, which step
         // s - 1 left before the last barrier; compute step s from stage
         // s % NST; wait for the loads of step s + 1 and barrier.
@@ -506,12 +508,32 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     } else {
         // round r: group wk loads step 2r + 2 + wk into the stage that its
         // step 2r - 2 + wk left and computes step 2r + wk; both steps of the
-        // next round land before the barrier.
-        for (int r = 0; KS * r < nsteps; ++r) {
-            const int sl = KS * r + KS + wk, sc = KS * r + wk;
-            dma(sl, sl % NST);
-            if (sc < nsteps) compute(sc, sc % NST);
-            step_barrier<0>();
+        // next round land before the barrier.  A group only ever uses stages
+        // wk and wk + 2, so (up to 3 columns per wave) rounds run in pairs
+        // with the stage parity fixed at compile time: each fragment address
+        // is then a loop-invariant lane address plus a constant (the
+        // instruction's offset field), not a per-step addition.
+        static_assert(KS == 2 && NST == 4, "two groups on a ring of four stages");
+        if constexpr (TN <= 3) {
+            auto round = [&](auto parity, int r) {
+                constexpr int P = decltype(parity)::value;
+                const int sl = 2 * r + 2 + wk, sc = 2 * r + wk;
+                dma(sl, wk + 2 * (1 - P));
+                if (sc < nsteps) compute(sc, wk + 2 * P);
+                step_barrier<0>();
+            };
+            for (int r = 0; 2 * r < nsteps; r += 2) {
+                round(std::integral_constant<int, 0>{}, r);
+                if (2 * (r + 1) >= nsteps) break;
+                round(std::integral_constant<int, 1>{}, r + 1);
+            }
+        } else {  // wider tiles: no registers for the extra lane addresses
+            for (int r = 0; KS * r < nsteps; ++r) {
+                const int sl = KS * r + KS + wk, sc = KS * r + wk;
+                dma(sl, sl % NST);
+                if (sc < nsteps) compute(sc, sc % NST);
+                step_barrier<0>();
+            }
         }
     }
     // no direct-to-LDS load may outlive the workgroup
