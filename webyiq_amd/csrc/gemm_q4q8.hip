@@ -102,6 +102,17 @@ __device__ __forceinline__ void dma4(const void* base, uint32_t off, const void*
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
                  ::"v"(off), "s"(uniform_ptr(base)), "s"(lds_addr(lds)) : "memory", "m0");
 }
+// The same with the LDS destination given as a wave-uniform 32-bit LDS byte
+// address (kept in scalar registers by the caller: no per-load conversion of
+// a generic pointer).
+__device__ __forceinline__ void dma16_at(const void* base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 ::"v"(off), "s"(uniform_ptr(base)), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4_at(const void* base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+                 ::"v"(off), "s"(uniform_ptr(base)), "s"(lds) : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Threads of a workgroup: the per-token group-128 format runs two groups of
@@ -242,26 +253,31 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     }
     // Every load is unconditional (steps past the end re-read the last one),
     // so each call issues exactly VM vector-memory instructions per wave.
+    // LDS byte address of the ring (scalar); stage st, part at byte b of it
+    const uint32_t lds0 = lds_addr(lds);
+    auto stage_at = [&](int st, int b) -> uint32_t { return lds0 + (uint32_t)(st * ST_SZ + b); };
     auto dma = [&](int step, const int st) {
         step = step < nsteps ? step : nsteps - 1;
         const int8_t* xq = a.xq + step * kBK;
         const uint8_t* wq = reinterpret_cast<const uint8_t*>(a.wq) + step * (kBK / 2);
         const uint32_t* ws = a.ws + step * NGS;
 #pragma unroll
-        for (int i = 0; i < A_PW; ++i) dma16(xq, a_off[i], As(st) + 1024 * (A_PW * wave + i));
+        for (int i = 0; i < A_PW; ++i) dma16_at(xq, a_off[i], stage_at(st, 1024 * (A_PW * wave + i)));
 #pragma unroll
-        for (int i = 0; i < B_PW; ++i) dma16(wq, b_off[i], Bs(st) + 256 * (B_PW * wave + i));
+        for (int i = 0; i < B_PW; ++i) dma16_at(wq, b_off[i], stage_at(st, A_SZ + 1024 * (B_PW * wave + i)));
 #pragma unroll
-        for (int i = 0; i < S_PW; ++i) dma4(ws, 4 * s_off[i], Ss(st) + 64 * (S_PW * wave + i));
+        for (int i = 0; i < S_PW; ++i) dma4_at(ws, 4 * s_off[i], stage_at(st, A_SZ + B_SZ + 256 * (S_PW * wave + i)));
         if constexpr (!FAST) {
             const int32_t* xs = a.xs + step * NES;
 #pragma unroll
-            for (int i = 0; i < X_PW; ++i) dma4(xs, 4 * x_off[i], Xs(st) + 64 * (X_PW * wave + i));
+            for (int i = 0; i < X_PW; ++i)
+                dma4_at(xs, 4 * x_off[i], stage_at(st, A_SZ + B_SZ + S_SZ + 256 * (X_PW * wave + i)));
         }
         if constexpr (!PT) {
             const float* dxp = a.dx + step * NES;
 #pragma unroll
-            for (int i = 0; i < D_PW; ++i) dma4(dxp, 4 * d_off[i], Ds(st) + 64 * (D_PW * wave + i));
+            for (int i = 0; i < D_PW; ++i)
+                dma4_at(dxp, 4 * d_off[i], stage_at(st, A_SZ + B_SZ + S_SZ + X_SZ + 256 * (D_PW * wave + i)));
         }
     };
 
