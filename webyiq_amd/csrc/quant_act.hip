@@ -17,8 +17,9 @@
 // same value, so codes are bit-identical across the kernels below and the
 // fused GEMV quantiser.
 //
-// Two layouts: few tokens -- one workgroup per token, wave w taking loads 2w
-// and 2w + 1 of every pass (latency); many tokens -- one wavefront per token,
+// Two layouts: few tokens -- one workgroup of eight waves per token, wave w
+// taking load w of every pass (latency: 1.0 us less than four waves with
+// the RMSNorm, 0.5 us without); many tokens -- one wavefront per token,
 // four tokens per workgroup, no barriers (throughput).
 #include "common.hpp"
 #include "launch.hpp"
@@ -76,9 +77,16 @@ __device__ __forceinline__ void emit(const QuantArgs& a, int64_t t, int c, bool 
     }
 }
 
-// One workgroup per token; wave w holds loads 2w, 2w + 1 of every pass.
-template <bool NORM, bool PER_TOKEN, int GE>
-__global__ __launch_bounds__(kQuantThreads) void quant_split_kernel(QuantArgs a) {
+// One workgroup of QW = 4 or 8 waves per token; wave w holds loads
+// LPW w .. LPW w + LPW - 1 of every pass (LPW = 8 / QW).  The per-wave
+// RMSNorm subtotals meet in the lane tree's own order: with four waves each
+// holds a pair (c0 + c1, ...) and they meet as (s0 + s1) + (s2 + s3); with
+// eight each holds one chunk and they meet as ((s0 + s1) + (s2 + s3)) +
+// ((s4 + s5) + (s6 + s7)).
+template <bool NORM, bool PER_TOKEN, int GE, int QW>
+__global__ __launch_bounds__(64 * QW) void quant_split_kernel(QuantArgs a) {
+    static_assert(QW == 4 || QW == 8, "waves per token");
+    constexpr int LPW = 8 / QW;  // loads per wave and pass
     pin_arg(a.x); pin_arg(a.norm_w); pin_arg(a.eps); pin_arg(a.K);
     pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -88,17 +96,18 @@ __global__ __launch_bounds__(kQuantThreads) void quant_split_kernel(QuantArgs a)
     const int J = (nchunk + kPassChunks - 1) / kPassChunks;
     const float4* xr = reinterpret_cast<const float4*>(a.x + t * a.K);
     const float4* nw = reinterpret_cast<const float4*>(a.norm_w);
-    __shared__ float sub[kSplitMaxPasses][kQuantWaves][64];  // per-wave lane subtrees
+    __shared__ float sub[kSplitMaxPasses][QW][64];  // per-wave lane subtotals
     __shared__ float red[kSplitMaxPasses];
-    __shared__ float wred[kQuantWaves];
+    __shared__ float wred[QW];
     const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto chunk = [&](int j, int i) { return kPassChunks * j + 64 * (LPW * wave + i) + lane; };
 
-    float4 xc[kSplitMaxPasses][2], wc[kSplitMaxPasses][2];
+    float4 xc[kSplitMaxPasses][LPW], wc[kSplitMaxPasses][LPW];
 #pragma unroll
     for (int j = 0; j < kSplitMaxPasses; ++j)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int c = kPassChunks * j + 64 * (2 * wave + i) + lane;
+        for (int i = 0; i < LPW; ++i) {
+            const int c = chunk(j, i);
             const bool ok = j < J && c < nchunk;
             xc[j][i] = ok ? xr[c] : zero4;
             if (NORM) wc[j][i] = ok ? nw[c] : zero4;
@@ -108,14 +117,17 @@ __global__ __launch_bounds__(kQuantThreads) void quant_split_kernel(QuantArgs a)
     if (NORM) {
 #pragma unroll
         for (int j = 0; j < kSplitMaxPasses; ++j)
-            if (j < J) sub[j][wave][lane] = chunk_ss(xc[j][0]) + chunk_ss(xc[j][1]);
+            if (j < J) sub[j][wave][lane] = LPW == 2 ? chunk_ss(xc[j][0]) + chunk_ss(xc[j][LPW - 1]) : chunk_ss(xc[j][0]);
         __syncthreads();
-        // wave w completes passes w, w + 4: the lane tree, then the lane tree
+        // wave w completes passes w, w + QW, ...: the lane tree, then the lane tree
 #pragma unroll
-        for (int q = 0; q < kSplitMaxPasses / kQuantWaves; ++q) {
-            const int j = wave + kQuantWaves * q;
+        for (int q = 0; q < (kSplitMaxPasses + QW - 1) / QW; ++q) {
+            const int j = wave + QW * q;
             if (j < J) {
-                const float p = (sub[j][0][lane] + sub[j][1][lane]) + (sub[j][2][lane] + sub[j][3][lane]);
+                const float* sj = &sub[j][0][lane];
+                float p;
+                if (QW == 4) p = (sj[0] + sj[64]) + (sj[128] + sj[192]);
+                else p = ((sj[0] + sj[64]) + (sj[128] + sj[192])) + ((sj[256] + sj[320]) + (sj[384] + sj[448]));
                 const float s = wave_sum_tree(p);
                 if (lane == 0) red[j] = s;
             }
@@ -132,14 +144,16 @@ __global__ __launch_bounds__(kQuantThreads) void quant_split_kernel(QuantArgs a)
 #pragma unroll
         for (int j = 0; j < kSplitMaxPasses; ++j)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int c = kPassChunks * j + 64 * (2 * wave + i) + lane;
+            for (int i = 0; i < LPW; ++i) {
+                const int c = chunk(j, i);
                 if (j < J && c < nchunk) m = fmaxf(m, absmax4(NORM ? normed(xc[j][i], r, wc[j][i]) : xc[j][i]));
             }
         m = wave_max(m);
         if (lane == 0) wred[wave] = m;
         __syncthreads();
-        const float amax = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+        float amax = wred[0];
+#pragma unroll
+        for (int w = 1; w < QW; ++w) amax = fmaxf(amax, wred[w]);
         dtok = amax / 127.0f;
         if (tid == 0) a.dx[t] = dtok;
     }
@@ -148,8 +162,8 @@ __global__ __launch_bounds__(kQuantThreads) void quant_split_kernel(QuantArgs a)
     for (int j = 0; j < kSplitMaxPasses; ++j) {
         if (j >= J) break;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int c = kPassChunks * j + 64 * (2 * wave + i) + lane;
+        for (int i = 0; i < LPW; ++i) {
+            const int c = chunk(j, i);
             const float4 v = NORM ? normed(xc[j][i], r, wc[j][i]) : xc[j][i];
             emit<PER_TOKEN, GE>(a, t, c, c < nchunk, v, dtok, rtok, lane);
         }
@@ -348,7 +362,11 @@ template <bool NORM, bool PT, int GE>
 hipError_t dispatch_rows(const QuantArgs& a, hipStream_t s) {
     const int64_t passes = (a.K + 4 * kPassChunks - 1) / (4 * kPassChunks);
     if (a.M <= kSplitMaxTokens && passes <= kSplitMaxPasses) {
-        hipLaunchKernelGGL((quant_split_kernel<NORM, PT, GE>), dim3((unsigned)a.M), dim3(kQuantThreads), 0, s, a);
+#ifndef WQ_QUANT_SPLIT_WAVES
+#define WQ_QUANT_SPLIT_WAVES 8
+#endif
+        hipLaunchKernelGGL((quant_split_kernel<NORM, PT, GE, WQ_QUANT_SPLIT_WAVES>), dim3((unsigned)a.M),
+                           dim3(64 * WQ_QUANT_SPLIT_WAVES), 0, s, a);
         return hipGetLastError();
     }
     dim3 grid((unsigned)((a.M + kQuantWaves - 1) / kQuantWaves)), block(kQuantThreads);
