@@ -358,6 +358,82 @@ __global__ __launch_bounds__(kQuantThreads) void mtp_in_kernel(MtpInArgs a) {
     });
 }
 
+// MTP input stage for rows of at most kSplitMaxPasses passes: one workgroup
+// of eight waves per (token, half), wave w holding load w of every pass (the
+// few-token quantiser's split).  The sums of squares meet in the lane tree's
+// order through LDS, as in quant_split_kernel, so the codes are
+// bit-identical to mtp_in_kernel's.
+__global__ __launch_bounds__(512) void mtp_in_split_kernel(MtpInArgs a) {
+    constexpr int QW = 8;
+    pin_arg(a.emb); pin_arg(a.x); pin_arg(a.norm_f); pin_arg(a.norm_e); pin_arg(a.norm_h);
+    pin_arg(a.eps); pin_arg(a.K); pin_arg(a.M); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t row = blockIdx.x;  // output row 2m + half
+    const int64_t m = row >> 1;
+    const bool hidden = (row & 1) != 0;
+    const int K = (int)a.K;
+    const int nchunk = K / 4;
+    const int J = (nchunk + kPassChunks - 1) / kPassChunks;
+    const float4* src = reinterpret_cast<const float4*>((hidden ? a.x : a.emb) + m * a.K);
+    const float4* w0 = reinterpret_cast<const float4*>(hidden ? a.norm_f : a.norm_e);
+    const float4* w1 = reinterpret_cast<const float4*>(a.norm_h);
+    __shared__ float sub[kSplitMaxPasses][QW][64];
+    __shared__ float red[kSplitMaxPasses];
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto chunk = [&](int j) { return kPassChunks * j + 64 * wave + lane; };
+
+    float4 xc[kSplitMaxPasses], wc0[kSplitMaxPasses], wc1[kSplitMaxPasses];
+#pragma unroll
+    for (int j = 0; j < kSplitMaxPasses; ++j) {
+        const int c = chunk(j);
+        const bool ok = j < J && c < nchunk;
+        xc[j] = ok ? src[c] : zero4;
+        wc0[j] = ok ? w0[c] : zero4;
+        wc1[j] = ok && hidden ? w1[c] : zero4;
+    }
+    auto scale = [](float4 v, float r, float4 w) {  // mtp_in.wgsl:56,65,70: v *= r * w
+        v.x = v.x * (r * w.x);
+        v.y = v.y * (r * w.y);
+        v.z = v.z * (r * w.z);
+        v.w = v.w * (r * w.w);
+        return v;
+    };
+    // 1 / rms of the values vals(j) (mtp_in.wgsl:26-42), the lane tree's order
+    auto inv_rms = [&](auto&& vals) {
+#pragma unroll
+        for (int j = 0; j < kSplitMaxPasses; ++j)
+            if (j < J) sub[j][wave][lane] = chunk_ss(vals(j));
+        __syncthreads();
+        // wave w completes pass w: the tree over the waves, then over the lanes
+        if (wave < J) {
+            const float* sj = &sub[wave][0][lane];
+            const float p = ((sj[0] + sj[64]) + (sj[128] + sj[192])) + ((sj[256] + sj[320]) + (sj[384] + sj[448]));
+            const float ps = wave_sum_tree(p);
+            if (lane == 0) red[wave] = ps;
+        }
+        __syncthreads();
+        float total = 0.0f;
+        for (int j = 0; j < J; ++j) total = total + red[j];
+        return 1.0f / sqrt_rn(mean_of(total, K) + a.eps);
+    };
+    const float r0 = inv_rms([&](int j) { return xc[j]; });
+    float r1 = 0.0f;
+    if (hidden) r1 = inv_rms([&](int j) { return scale(xc[j], r0, wc0[j]); });  // uniform per workgroup
+
+    QuantArgs q{};
+    q.K = a.K;
+    q.xq = a.xq;
+    q.dx = a.dx;
+    q.xs = a.xs;
+#pragma unroll
+    for (int j = 0; j < kSplitMaxPasses; ++j) {
+        if (j >= J) break;
+        const int c = chunk(j);
+        const float4 v0 = scale(xc[j], r0, wc0[j]);
+        emit<false, 32>(q, row, c, c < nchunk, hidden ? scale(v0, r1, wc1[j]) : v0, 0.0f, 0.0f, lane);
+    }
+}
+
 template <bool NORM, bool PT, int GE>
 hipError_t dispatch_rows(const QuantArgs& a, hipStream_t s) {
     const int64_t passes = (a.K + 4 * kPassChunks - 1) / (4 * kPassChunks);
@@ -396,6 +472,10 @@ hipError_t launch_quant_act(const QuantArgs& a, hipStream_t s) {
 
 hipError_t launch_mtp_in(const MtpInArgs& a, hipStream_t s) {
     const int64_t passes = (a.K + 4 * kPassChunks - 1) / (4 * kPassChunks);
+    if (passes <= kSplitMaxPasses && 2 * a.M <= 65535) {
+        hipLaunchKernelGGL(mtp_in_split_kernel, dim3((unsigned)(2 * a.M)), dim3(512), 0, s, a);
+        return hipGetLastError();
+    }
     dim3 grid((unsigned)((2 * a.M + kQuantWaves - 1) / kQuantWaves)), block(kQuantThreads);
     if (passes <= 1)
         hipLaunchKernelGGL((mtp_in_kernel<1>), grid, block, 0, s, a);
