@@ -68,6 +68,19 @@ __global__ __launch_bounds__(64 * kCombineWaves) void attn_combine_kernel(AttnCo
     float* w = sh;
     float* chains = sh + nch;
 
+    // The partials of this wave's first UNROLL chunks and (wave 0) the first
+    // weight sums do not depend on the maximum: their loads are issued with
+    // the maxima's, one memory round trip instead of two.
+    const float* pl = hb + DPL * lane;
+    float pf[UNROLL][DPL];
+#pragma unroll
+    for (int q = 0; q < UNROLL; ++q) {
+        const int cq = wave + kCombineWaves * q;
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) pf[q][k] = cq < n ? pl[(int64_t)cq * (D + 2) + k] : 0.0f;
+    }
+    const float lf = wave == 0 && lane < n ? hb[(int64_t)lane * (D + 2) + D + 1] : 0.0f;
+
     // chunk maxima (attn_combine.wgsl:39-42), in every wavefront
     float ml = -3.0e38f;
     for (int c = lane; c < n; c += 64) ml = fmaxf(ml, hb[(int64_t)c * (D + 2) + D]);
@@ -80,8 +93,16 @@ __global__ __launch_bounds__(64 * kCombineWaves) void attn_combine_kernel(AttnCo
     float acc[DPL];
 #pragma unroll
     for (int k = 0; k < DPL; ++k) acc[k] = 0.0f;
-    const float* pl = hb + DPL * lane;
-    int c = wave;
+#pragma unroll
+    for (int q = 0; q < UNROLL; ++q) {  // the prefetched chunks, in order
+        const int cq = wave + kCombineWaves * q;
+        if (cq < n) {
+            const float wc = w[cq];
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) acc[k] = fmaf(wc, pf[q][k], acc[k]);
+        }
+    }
+    int c = wave + kCombineWaves * UNROLL;
     for (; c + kCombineWaves * (UNROLL - 1) < n; c += kCombineWaves * UNROLL) {
         float p[UNROLL][DPL], wc[UNROLL];
 #pragma unroll
@@ -107,8 +128,10 @@ __global__ __launch_bounds__(64 * kCombineWaves) void attn_combine_kernel(AttnCo
     }
     // weight sum (:47), lane-parallel then the lane tree
     float ll = 0.0f;
-    if (wave == 0)
-        for (int cc = lane; cc < n; cc += 64) ll = fmaf(w[cc], hb[(int64_t)cc * (D + 2) + D + 1], ll);
+    if (wave == 0) {
+        if (lane < n) ll = fmaf(w[lane], lf, ll);
+        for (int cc = lane + 64; cc < n; cc += 64) ll = fmaf(w[cc], hb[(int64_t)cc * (D + 2) + D + 1], ll);
+    }
     __syncthreads();
     if (wave > 0) return;  // no barrier follows
     const float l = wave_sum_tree(ll);
