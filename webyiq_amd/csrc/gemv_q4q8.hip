@@ -15,7 +15,8 @@
 // so the whole matrix is in flight at once across the chip.
 //
 // Each lane computes its 32-code dot product with 8 v_dot4_i32_i8, a quad of
-// lanes (DPP) completes a 128-group; the exact int32 group sums go to LDS.
+// lanes (DPP) completes a 128-group; the exact int32 group sums stay in
+// registers (one token, per-token group 128) or go to LDS.
 // The fp32 epilogue folds each (token, row) in a fixed order the CPU oracle
 // restates, so outputs are bit-reproducible (modes 0 and 1) and the fused
 // argmax sees the same logits.  Per-token group-128 (the BASELINE format):
@@ -303,7 +304,9 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         }
     }
 
-    // fp32 epilogue: one chain per (token, row) over the groups in order
+    // fp32 epilogue of the formats other than per-token group 128 (which
+    // return below before using it): one chain per (token, row) over the
+    // groups in order
     auto chain = [&](int t, int h, int rl) -> float {
         const int32_t* ar = acc_lds + ((t * NH + h) * RB + rl) * NEP;
         const float2* sr = sm_lds + (h * RB + rl) * NGS;
