@@ -257,7 +257,11 @@ void or_group_acc(const uint32_t* wq, int64_t N, int64_t K, int Ge,
  *                        the pass sums added left to right; a = total * dx
  *   per token, G = 32:   one chain over e = 0, 1, ...:
  *                        acc = fma(s, A, acc); acc = fma(m, X, acc); a = acc * dx
- *   per 32   (GA = 32):  one chain: acc = fma(s*dx_e, A, acc); acc = fma(m*dx_e, X, acc); a = acc */
+ *   per 32   (GA = 32):  per pass of 2048 codes (64 groups of 32), sixteen
+ *                        chains, chain i over the groups 64p + 4i .. 64p + 4i + 3
+ *                        that exist: c = fma(s*dx_e, A, c); c = fma(m*dx_e, X, c)
+ *                        from c = 0; T_p = the pairwise tree over c_0 .. c_15;
+ *                        the pass sums added left to right; a = total */
 static float row_value(const uint32_t* wrow, const uint32_t* srow, int64_t K, int G, int GA,
                        const int8_t* xrow, const float* dxrow, const int32_t* xsrow) {
     int Ge = GA < G ? GA : G;
@@ -287,6 +291,34 @@ static float row_value(const uint32_t* wrow, const uint32_t* srow, int64_t K, in
             total = e0 == 0 ? t : total + t;
         }
         return total * dxrow[0];
+    }
+    if (GA < K) {
+        float total = 0.0f;
+        for (int64_t e0 = 0; e0 < NE; e0 += 64) {
+            float c[16];
+            for (int q = 0; q < 16; ++q) {
+                c[q] = 0.0f;
+                for (int k = 0; k < 4; ++k) {
+                    int64_t e = e0 + 4 * q + k;
+                    if (e >= NE) break;
+                    int32_t a = 0;
+                    for (int i = 0; i < Ge; ++i) {
+                        int64_t kk = e * Ge + i;
+                        a += (int32_t)code(wrow, kk) * (int32_t)xrow[kk];
+                    }
+                    uint32_t sw = srow[(e * Ge) / G];
+                    float s = or_f16_to_f32((uint16_t)(sw & 0xFFFFu));
+                    float m = or_f16_to_f32((uint16_t)(sw >> 16));
+                    float d = dxrow[e];
+                    c[q] = fmaf(s * d, (float)a, c[q]);
+                    c[q] = fmaf(m * d, (float)xsrow[e], c[q]);
+                }
+            }
+            for (int w = 16; w > 1; w /= 2)
+                for (int k = 0; k < w / 2; ++k) c[k] = c[2 * k] + c[2 * k + 1];
+            total = e0 == 0 ? c[0] : total + c[0];
+        }
+        return total;
     }
     float acc = 0.0f;
     for (int64_t e = 0; e < NE; ++e) {

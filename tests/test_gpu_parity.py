@@ -280,7 +280,9 @@ def test_gemm_bit_exact(M, K, N, G, GA, mode):
     y, acc = ops.group_sums(ops.PATH_PREFILL, w, a, mode=mode, y=dev(y0) if mode == 1 else None)
     assert np.array_equal(host(acc), acc_want)
     got = host(y)
-    if mode == 2 or (G == 128 and GA is None):
+    if mode == 2 or (G == 128 and GA is None) or GA == 32:
+        # f16-MFMA min term, device expf, or (per-32 activations) the GEMM's
+        # single fold chain against the GEMV's chains-and-tree order
         assert rel_err(got, want) < 1e-5
     else:
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
@@ -323,7 +325,7 @@ def test_gemm_wide_tiles(K, N, G, GA, mode):
                                     np.arange(0, M, 8) + (np.arange(0, M, 8) // 128) % 8]))
     want = oracle_linear_tokens(wq, ws, K, G, xq[idx], dx[idx], xs[idx], mode=mode,
                                 y=y0[idx] if mode == 1 else None, GA=gaa)
-    if mode == 2 or (G == 128 and GA is None):
+    if mode == 2 or (G == 128 and GA is None) or GA == 32:
         assert rel_err(got[idx], want) < 1e-5
     else:
         assert np.array_equal(got[idx].view(np.uint32), want.view(np.uint32))

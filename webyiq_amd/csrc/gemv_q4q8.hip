@@ -24,8 +24,11 @@
 // c = fma(m, X, c) over the pairs of groups (2i, 2i + 1), the pairwise tree
 // over the 8 pair values, the pass sums added in order -- for one token in
 // registers (DPP moves across the wave's quads, no LDS round trip when a
-// row is one pass), for more through LDS, four lanes per (token, row).  The
-// other formats: one fma chain per (token, row) over the groups in order.
+// row is one pass), for more through LDS, four lanes per (token, row).
+// Per-32 activation scales: per pass of 64 groups of 32, sixteen chains over
+// four consecutive groups and the pairwise tree over them, four lanes per
+// (token, row).  Per-token group 32: one fma chain per (token, row) over the
+// groups in order.
 #include "argmax_combine.hpp"
 #include "common.hpp"
 #include "launch.hpp"
@@ -304,9 +307,9 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         }
     }
 
-    // fp32 epilogue of the formats other than per-token group 128 (which
-    // return below before using it): one chain per (token, row) over the
-    // groups in order
+    // fp32 epilogue of the per-token group-32 format (per-token group 128 and
+    // per-32 activations return below before using it): one chain per
+    // (token, row) over the groups in order
     auto chain = [&](int t, int h, int rl) -> float {
         const int32_t* ar = acc_lds + ((t * NH + h) * RB + rl) * NEP;
         const float2* sr = sm_lds + (h * RB + rl) * NGS;
@@ -364,26 +367,8 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
             }
             return acc * dr[0];
         } else {
-            // per-32 activation scales: the same chain, its operands read four
-            // groups at a time (NE = K/32 is a multiple of 4)
-#pragma unroll 2
-            for (int ee = 0; ee < NE; ee += 4) {
-                const int4 a4 = *reinterpret_cast<const int4*>(ar + ee);
-                const float4 x4 = *reinterpret_cast<const float4*>(xsr + ee);
-                const float4 d4 = *reinterpret_cast<const float4*>(dr + ee);
-                float2 w[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) w[q] = sr[((ee + q) * 32) / G];
-                acc = fmaf(w[0].x * d4.x, (float)a4.x, acc);
-                acc = fmaf(w[0].y * d4.x, x4.x, acc);
-                acc = fmaf(w[1].x * d4.y, (float)a4.y, acc);
-                acc = fmaf(w[1].y * d4.y, x4.y, acc);
-                acc = fmaf(w[2].x * d4.z, (float)a4.z, acc);
-                acc = fmaf(w[2].y * d4.z, x4.z, acc);
-                acc = fmaf(w[3].x * d4.w, (float)a4.w, acc);
-                acc = fmaf(w[3].y * d4.w, x4.w, acc);
-            }
-            return acc;
+            (void)dr;
+            return acc;  // not reached: per-32 activations take the four-lane epilogue
         }
     };
     // y of (token t, local row rl) from its chain(s)
@@ -625,6 +610,95 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
                     *yo = *yo + v;
                 } else {
                     *yo = silu_mul(v, tot[NH - 1] * d);
+                }
+            }
+        }
+        if constexpr (ARGMAX) {
+            __syncthreads();
+            const unsigned long long best = block_best<MT>(keys, RB, (int)a.M);
+            argmax_combine<MT>(p.am, (int)a.M, p.nblocks, best);
+        }
+        return;
+    }
+
+    if constexpr (!PT) {
+        // Per-32 activation scales: four lanes per (token, row).  Per pass of
+        // 64 groups of 32, lane q runs the chains c = fma(s dx, A, c);
+        // c = fma(m dx, X, c) from 0 over groups 16q + 4i .. 16q + 4i + 3
+        // (i = 0..3) and forms (c0 + c1) + (c2 + c3); two quad moves complete
+        // the pairwise tree over the pass's 16 chains; the pass sums are
+        // added in order.  The oracle's order.
+        unsigned long long* keys = lds_align<8, unsigned long long>(smem, dx_lds + (size_t)MT * NDX);
+        for (int o = tid; o < 4 * MT * RB; o += nthreads) {
+            const int q = o & 3, oo = o >> 2;
+            const int t = oo / RB, rl = oo - t * RB;
+            const float* xsr = xs_lds + t * NE;
+            const float* dr = dx_lds + t * NDX;
+            float tot[NH];
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const int32_t* ar = acc_lds + ((t * NH + h) * RB + rl) * NEP;
+                const float2* sr = sm_lds + (h * RB + rl) * NGS;
+                float total = 0.0f;
+                for (int e0 = 0; e0 < NE; e0 += 64) {
+                    float c[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int eb = e0 + 16 * q + 4 * i;  // NE is a multiple of 4
+                        float v = 0.0f;
+                        if (eb < NE) {
+                            const int4 a4 = *reinterpret_cast<const int4*>(ar + eb);
+                            const float4 x4 = *reinterpret_cast<const float4*>(xsr + eb);
+                            const float4 d4 = *reinterpret_cast<const float4*>(dr + eb);
+                            float2 w0, w1, w2, w3;
+                            if constexpr (G == 128) {  // the four groups share one weight group
+                                w0 = w1 = w2 = w3 = sr[eb / 4];
+                            } else {
+                                const float4 w01 = *reinterpret_cast<const float4*>(sr + eb);
+                                const float4 w23 = *reinterpret_cast<const float4*>(sr + eb + 2);
+                                w0 = make_float2(w01.x, w01.y);
+                                w1 = make_float2(w01.z, w01.w);
+                                w2 = make_float2(w23.x, w23.y);
+                                w3 = make_float2(w23.z, w23.w);
+                            }
+                            v = fmaf(w0.x * d4.x, (float)a4.x, v);
+                            v = fmaf(w0.y * d4.x, x4.x, v);
+                            v = fmaf(w1.x * d4.y, (float)a4.y, v);
+                            v = fmaf(w1.y * d4.y, x4.y, v);
+                            v = fmaf(w2.x * d4.z, (float)a4.z, v);
+                            v = fmaf(w2.y * d4.z, x4.z, v);
+                            v = fmaf(w3.x * d4.w, (float)a4.w, v);
+                            v = fmaf(w3.y * d4.w, x4.w, v);
+                        }
+                        c[i] = v;
+                    }
+                    float v = (c[0] + c[1]) + (c[2] + c[3]);
+                    v = v + dpp_f<kDppXor1>(v);
+                    v = v + dpp_f<kDppXor2>(v);
+                    total = e0 == 0 ? v : total + v;
+                }
+                tot[h] = total;
+            }
+            if (q != 0) continue;
+            const int64_t row = r0 + rl;
+            const bool ok = t < a.M && row < N;
+            if constexpr (ARGMAX) {
+                unsigned long long key = 0;
+                if (ok) {
+                    const float v = tot[0];
+                    if (a.y) a.y[(int64_t)t * N + row] = v;
+                    if (v > -3.0e38f) key = argmax_key(v, (uint32_t)row);
+                }
+                keys[t * RB + rl] = key;
+            } else if (ok) {
+                float* yo = a.y + (int64_t)t * N + row;
+                const float v = tot[0];
+                if (MODE == 0) {
+                    *yo = v;
+                } else if (MODE == 1) {
+                    *yo = *yo + v;
+                } else {
+                    *yo = silu_mul(v, tot[NH - 1]);
                 }
             }
         }
