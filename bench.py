@@ -56,6 +56,10 @@ def parse():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-config lines (decode MLP, verify shapes, lm_head)")
     ap.add_argument("--cpu-seconds", type=float, default=24.0)
+    ap.add_argument("--gemm-copies", type=int, default=16,
+                    help="weight/output copies the prefill GEMMs rotate over (16 = 504 MB, twice the MALL)")
+    ap.add_argument("--gemm-warmup", type=int, default=400,
+                    help="graph replays before the prefill GEMMs are timed (clocks settle within ~80 ms)")
     ap.add_argument("--floor", action="store_true",
                     help="also time the no-arithmetic kernels of bench_floor.hip on the GEMV's grid "
                          "and weight copies, alternating with the GEMV (per-launch floors)")
@@ -263,7 +267,7 @@ def bench_gemm(torch, lib, ops, orc, ref, args):
         rng = np.random.default_rng(args.seed + K)
         wq, ws = ref.make_weight(rng, N, K, 128)
         x = ref.make_activations(rng, M, K)
-        copies = 16  # 16 x (6.3 MB weights + 25.2 MB outputs) = 504 MB, twice the MALL
+        copies = max(1, args.gemm_copies)  # 16: 16 x (6.3 MB weights + 25.2 MB outputs) = 504 MB
         q = [torch.from_numpy(wq.view(np.int32)).cuda() for _ in range(copies)]
         s = [torch.from_numpy(ws.view(np.int32)).cuda() for _ in range(copies)]
         a = ops.quant(torch.from_numpy(x).cuda(), G=128)
@@ -284,7 +288,7 @@ def bench_gemm(torch, lib, ops, orc, ref, args):
                                               M, K, 0, P(ys[i].data_ptr())]) for i in range(copies)]
         # warm-up long enough for the clocks to settle (the first ~30-80 ms
         # of MFMA load run measurably slower), then the median of three timings
-        graph_time(torch, launches, 400)
+        graph_time(torch, launches, max(1, args.gemm_warmup))
         t = float(np.median([graph_time(torch, launches, 25) for _ in range(3)]))
         ops_ = 2.0 * M * N * K
         res[f"K{K}_N{N}"] = {
