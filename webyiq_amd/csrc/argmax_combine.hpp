@@ -45,8 +45,15 @@ constexpr unsigned kArgmaxSpinLimit = 1u << 22;
 // last) merges its keys, takes a ticket in its slot and ends: its waves
 // past the first leave at once, the first waits for one atomic.  The last
 // workgroup merges its own keys, waits until every slot counts all of its
-// other workgroups, then reduces the slots, writes the token (mapped through
-// ids when set) and clears the workspace for the next call.
+// other workgroups, then reduces the slots (one wave per token, a lane per
+// slot), writes the token (mapped through ids when set) and clears the
+// workspace for the next call.
+//
+// A variant without tickets (a key line per workgroup, published with one
+// store and polled by the last workgroup until non-zero) was measured slower
+// on the large heads (31.3 -> 37.3 us at 151,936 rows, one token; 40.4 ->
+// 64.6 us at 8 tokens): the last workgroup's scans of every line, repeated
+// while the stream still runs, load the device's coherence point.
 //
 // Ordering without release fences.  A release fence at agent scope writes
 // back the whole L2 of the workgroup's XCD (the 8 XCDs' L2s are not coherent
@@ -103,7 +110,6 @@ __device__ __forceinline__ void argmax_combine(const ArgmaxArgs& am, int M, int 
         return;
     }
 
-    __shared__ unsigned long long slot_keys[kArgmaxSlots * MT];
     __shared__ unsigned int timed_out;
     const int used = nblocks < kArgmaxSlots ? nblocks : kArgmaxSlots;
     if (tid < 64) {
@@ -128,24 +134,26 @@ __device__ __forceinline__ void argmax_combine(const ArgmaxArgs& am, int M, int 
     }
     __syncthreads();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    // every slot key read at once (independent device-coherent loads), then
-    // reduced in LDS
-    for (int o = tid; o < used * MT; o += nthreads)
-        slot_keys[o] = __hip_atomic_load(am.keys + (o / MT) * kArgmaxSlotWords + (o % MT), __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (tid < M) {
-        unsigned long long k = 0;
-        for (int sl = 0; sl < used; ++sl) k = slot_keys[sl * MT + tid] > k ? slot_keys[sl * MT + tid] : k;
-        uint32_t idx = k ? 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull) : 0u;
-        am.tok_out[tid] = timed_out ? 0xFFFFFFFFu : am.ids ? am.ids[idx] : idx;
+    // Wave w reduces tokens w, w + nwaves, ...: lane l reads slot l's key
+    // (independent device-coherent loads), a 64-lane maximum (exact,
+    // order-free), and each lane then clears the key it read.
+    const int wave = tid >> 6, lane = tid & 63, nwaves = nthreads >> 6;
+    for (int t = wave; t < M && t < MT; t += nwaves) {
+        unsigned long long* kp = am.keys + lane * kArgmaxSlotWords + t;
+        unsigned long long k = lane < used ? __hip_atomic_load(kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const unsigned long long u = __shfl_xor(k, o, 64);
+            k = u > k ? u : k;
+        }
+        if (lane == 0) {
+            const uint32_t idx = k ? 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull) : 0u;
+            am.tok_out[t] = timed_out ? 0xFFFFFFFFu : am.ids ? am.ids[idx] : idx;
+        }
+        if (lane < used) __hip_atomic_store(kp, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __syncthreads();
-    for (int o = tid; o < used * MT; o += nthreads)
-        __hip_atomic_store(am.keys + (o / MT) * kArgmaxSlotWords + (o % MT), 0ull, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    for (int o = tid; o < used; o += nthreads)
-        __hip_atomic_store(am.ticket + o * kArgmaxSlotWords * 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < used)
+        __hip_atomic_store(am.ticket + tid * kArgmaxSlotWords * 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace wq
