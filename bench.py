@@ -63,6 +63,9 @@ def parse():
     ap.add_argument("--floor", action="store_true",
                     help="also time the no-arithmetic kernels of bench_floor.hip on the GEMV's grid "
                          "and weight copies, alternating with the GEMV (per-launch floors)")
+    ap.add_argument("--timeline", action="store_true",
+                    help="also replay the GEMV from the timing build (libwebyiq_q4q8_timeline.so) and "
+                         "report its per-workgroup phase stamps")
     ap.add_argument("--calib-mib", type=int, default=0,
                     help="after the timed region, copy a buffer of this many MiB 8 times "
                          "(the known-size kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -200,6 +203,9 @@ def main():
     if args.floor:
         out["floor"] = bench_floor(torch, launches, qs, ss, N)
 
+    if args.timeline:
+        out["timeline"] = bench_timeline(torch, [ln.args for ln in launches])
+
     if args.calib_mib > 0:
         nb = args.calib_mib << 20
         src = torch.empty(nb // 4, dtype=torch.float32, device=dev).fill_(1.0)
@@ -254,8 +260,54 @@ def bench_floor(torch, gemv_launches, qs, ss, N):
             times[k].append(graph_time(torch, lns, 20) * 1e6)
     res = {f"{k}_us": round(float(np.median(v)), 3) for k, v in times.items()}
     res["grid"] = "768 workgroups x 4 waves, 2 rows per wave (the GEMV's plan at M=1, K=2048, N=6144)"
+    # the empty kernel on other grids (256 threads each): per-launch cost against grid size
+    res["empty_us_by_workgroups"] = {}
+    for nwg in (1, 256, 768, 1536, 3072, 4096):
+        lns = [Floor(3, 0) for _ in range(R)]
+        for ln in lns:
+            ln.args = (3, P(qs[0].data_ptr()), P(ss[0].data_ptr()), P(out.data_ptr()), nwg)
+        graph_time(torch, lns, 5)
+        res["empty_us_by_workgroups"][str(nwg)] = round(graph_time(torch, lns, 20) * 1e6, 3)
     res["bytes_read"] = int(N * (1024 + 64))
     return res
+
+
+def bench_timeline(torch, launch_args):
+    """Phase stamps of the headline GEMV: the same launches (weight copies,
+    activations, output) from the timing build, libwebyiq_q4q8_timeline.so
+    (the kernels plus s_memrealtime stamps by thread 0 of each workgroup, a
+    100 MHz clock), replayed as graphs; the stamps are those of the last
+    launch.  Times in us from the first workgroup's entry, percentiles over
+    the workgroups.  The per-launch time is the timing build's own."""
+    from webyiq_amd import _lib
+    path = os.path.join(HERE, "webyiq_amd", "libwebyiq_q4q8_timeline.so")
+    if not os.path.exists(path):
+        print("bench.py: --timeline needs webyiq_amd/libwebyiq_q4q8_timeline.so (python -m webyiq_amd.build)",
+              file=sys.stderr)
+        sys.exit(1)
+    T = ctypes.CDLL(path)
+    T.wq_gemv.argtypes, T.wq_gemv.restype = _lib.PROTOTYPES["wq_gemv"]
+    T.wq_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    T.wq_timeline_read.restype = ctypes.c_int
+    launches = [Launcher(T, "wq_gemv", list(a)) for a in launch_args]
+    graph_time(torch, launches, 10)
+    t = graph_time(torch, launches, 20)
+    buf = np.zeros(4096 * 8, dtype=np.uint64)
+    if T.wq_timeline_read(buf.ctypes.data, buf.nbytes) != 0:
+        raise RuntimeError("wq_timeline_read failed")
+    b = buf.reshape(4096, 8).astype(np.int64)
+    b = b[b[:, 0] > 0]
+    t0 = b[:, 0].min()
+    names = ["entry", "activations_landed", "first_row_landed", "products_done", "outputs_stored"]
+    phases = {}
+    for k, name in enumerate(names):
+        d = (b[:, k] - t0) / 100.0
+        phases[name] = {q: round(float(np.percentile(d, v)), 2) for q, v in
+                        (("min", 0), ("p10", 10), ("median", 50), ("p90", 90), ("max", 100))}
+    dur = (b[:, 4] - b[:, 0]) / 100.0
+    return {"us_per_launch": round(t * 1e6, 3), "workgroups": int(len(b)), "phases_us": phases,
+            "workgroup_duration_us": {"median": round(float(np.median(dur)), 2), "max": round(float(dur.max()), 2)},
+            "clock": "s_memrealtime, 100 MHz"}
 
 
 def bench_gemm(torch, lib, ops, orc, ref, args):

@@ -7,7 +7,9 @@
 //                 all issued before the first is used, folded by XOR per
 //                 lane, no store (a store guarded by the folded value keeps
 //                 the loads live);
-//   read_store -- the same loads, and one 4-byte result per row (y).
+//   read_store -- the same loads, and one 4-byte result per row (y);
+//   kind 3     -- the empty kernel on a given number of workgroups (the
+//                 dispatch cost against grid size).
 // They bound from below what any kernel that streams the same bytes in
 // one launch can reach; bench.py times them as the GEMV is timed (graph
 // replays rotating over the weight copies).
@@ -68,6 +70,8 @@ extern "C" int floor_launch(void* stream, int kind, const void* w, const void* w
     const int grid = grid_of(n);
     if (kind == 0)
         hipLaunchKernelGGL(floor_empty, dim3(grid), dim3(256), 0, s, (int*)out, grid);
+    else if (kind == 3)  // the empty kernel on n workgroups of 256 threads (dispatch cost against grid size)
+        hipLaunchKernelGGL(floor_empty, dim3(n), dim3(256), 0, s, (int*)out, n);
     else if (kind == 1)
         hipLaunchKernelGGL(floor_read<false>, dim3(grid), dim3(256), 0, s, (const v4u*)w, (const uint32_t*)ws,
                            (uint32_t*)out, n);

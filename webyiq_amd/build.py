@@ -23,6 +23,9 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libwebyiq_q4q8.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HOST_LIB = os.path.join(HERE, "libwebyiq_graph.so")
+# timing build: the same library with the GEMV's per-workgroup stamps (-DWQ_TIMELINE)
+TIMELINE_LIB = os.path.join(HERE, "libwebyiq_q4q8_timeline.so")
+TIMELINE_SOURCE = "gemv_q4q8.hip"
 CXX = os.environ.get("CXX", "g++")
 
 SOURCES = ["capi.hip", "quant_act.hip", "gemv_q4q8.hip", "gemv_mfma.hip", "gemm_q4q8.hip", "argmax.hip", "embed.hip",
@@ -49,6 +52,11 @@ def build(verbose=False):
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
+    tl_obj = os.path.join(BUILD, "gemv_q4q8_timeline.o")
+    cmd = [HIPCC, *CFLAGS, "-DWQ_TIMELINE", "-c", os.path.join(CSRC, TIMELINE_SOURCE), "-o", tl_obj]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    procs.append((TIMELINE_SOURCE + " (timeline)", subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
     failed = []
     for src, p in procs:
         out, _ = p.communicate()
@@ -65,6 +73,10 @@ def build(verbose=False):
     tmp = LIB + ".tmp"
     subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp], check=True)
     os.replace(tmp, LIB)
+    tl_objs = [tl_obj if os.path.basename(o) == TIMELINE_SOURCE.replace(".hip", ".o") else o for o in objs]
+    tmp = TIMELINE_LIB + ".tmp"
+    subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *tl_objs, "-o", tmp], check=True)
+    os.replace(tmp, TIMELINE_LIB)
     build_host(verbose)
     return LIB
 

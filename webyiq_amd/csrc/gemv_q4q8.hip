@@ -36,6 +36,26 @@
 #pragma clang fp contract(off)
 
 namespace wq {
+
+#ifdef WQ_TIMELINE
+// Timing build only (-DWQ_TIMELINE: libwebyiq_q4q8_timeline.so, which
+// bench.py --timeline loads; the product library has none of this).  Thread
+// 0 of each of the first kTimelineWgs workgroups of the one-token plain GEMV
+// writes s_memrealtime (a 100 MHz clock) at five points: entry, its
+// activations landed, its first weight row landed, its rows' products done,
+// its outputs stored.  Each stamp adds a test of the value it marks, so it is
+// taken only once that value's load has returned.
+constexpr int kTimelineWgs = 4096;
+__device__ unsigned long long wq_timeline[kTimelineWgs * 8];
+#define WQ_STAMP(k, dep)                                                                              \
+    do {                                                                                              \
+        if (!QIN && !ARGMAX && MT == 1 && threadIdx.x == 0 && blockIdx.x < kTimelineWgs)              \
+            wq_timeline[blockIdx.x * 8 + (k)] = __builtin_amdgcn_s_memrealtime() + ((dep) == 0x7654321u); \
+    } while (0)
+#else
+#define WQ_STAMP(k, dep) ((void)0)
+#endif
+
 namespace {
 
 struct GemvParams {
@@ -82,6 +102,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         pin_arg(p.qin.xq); pin_arg(p.qin.dx); pin_arg(p.qin.xs);
     }
     const int tid = threadIdx.x;
+    WQ_STAMP(0, 0u);
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int NW = p.J * p.nslots;  // waves (blockDim.x / 64, without its late scalar load)
@@ -192,6 +213,10 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
             sv[h][s] = a.ws[(row + h * N) * NG + g];
         }
         asm volatile("" ::: "memory");  // loads stay in row order: row s lands before row s + 1
+    }
+    if constexpr (!QIN) {
+        WQ_STAMP(1, xa[0].x ^ xb[0].w ^ (uint32_t)xsv[0] ^ __float_as_uint(dxv[0]));
+        WQ_STAMP(2, wv[0][0].x ^ sv[0][0]);
     }
     if constexpr (QIN) {
         // Fused per-token quantiser, while the weight loads are in flight:
@@ -409,6 +434,14 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
                 }
             }
         }
+#ifdef WQ_TIMELINE
+        {
+            float all = 0.0f;
+#pragma unroll
+            for (int s = 0; s < IPW; ++s) all += vals[0][s][0];
+            WQ_STAMP(3, __float_as_uint(all));
+        }
+#endif
         unsigned long long* keys = lds_align<8, unsigned long long>(smem, dx_lds + (size_t)MT * NDX);
         // y (or the argmax key) of (token t, local row rl) from the row sums
         auto emit = [&](int t, int rl, float v0, float v1, float d) {
@@ -451,6 +484,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
                         rsel = slot + p.nslots * s;
                     }
             if (tsel >= 0) emit(tsel, rsel, v0, v1, dsel);
+            WQ_STAMP(4, 0u);
         } else {
             // pass sums [t][h][rl][pass] -> LDS, then each (token, row) adds
             // its passes left to right
@@ -896,3 +930,11 @@ hipError_t launch_gemv_quant_in(const LinearArgs& a, const QuantInArgs& q, hipSt
 }
 
 }  // namespace wq
+
+#ifdef WQ_TIMELINE
+// The stamps of the last launch (kTimelineWgs x 8 words) into host memory.
+extern "C" int wq_timeline_read(void* host, size_t bytes) {
+    const size_t n = sizeof(unsigned long long) * wq::kTimelineWgs * 8;
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(wq::wq_timeline), bytes < n ? bytes : n);
+}
+#endif
