@@ -289,10 +289,17 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
 }
 
 // K <= 2048 (at most 16 groups): every wave owns all groups of a 16-row
-// block, the group sums stay in the MFMA result registers and each lane runs
-// the fp32 chains of its row and four tokens there, in the LDS chain's order
-// (no group-sum buffer: ~27 KB of LDS, five workgroups per CU).  Measured
-// against 2 and 8 waves per workgroup, 4 is fastest.
+// block and each lane runs the fp32 chains of its row and four tokens in
+// registers, in the LDS chain's order (no group-sum buffer: ~27 KB of LDS,
+// five workgroups per CU).  The scale words are loaded before the weights,
+// so their exchange through LDS is done when the first weight group lands;
+// each group's two MFMAs and its fold step then run as soon as that group
+// lands (folding after the last group's MFMAs was 1-1.5 us slower on the
+// lm_head shapes).  Measured against 2 and 8 waves per workgroup, 4 is
+// fastest.  Splitting the fold between the wave's halves (MFMA rows 8..15
+// repeating tokens 0..7, odd pairs in the upper lanes, a lane exchange
+// before the tree) was measured much slower (38.9 -> 63.3 us at 8 tokens x
+// 151,936 rows) and is not used.
 template <int MT, int MODE, bool ARGMAX>
 __global__ __launch_bounds__(64 * kRowsWaves) void gemv_mfma_rows_kernel(MfmaGemvParams p) {
     constexpr int NH = MODE == 2 ? 2 : 1;
@@ -336,8 +343,17 @@ __global__ __launch_bounds__(64 * kRowsWaves) void gemv_mfma_rows_kernel(MfmaGem
     {
         const int64_t rr = (int64_t)blockIdx.x * RB + 16 * wave + c;  // this lane's row
         const int64_t row = rr < N ? rr : N - 1;
-        uint4 wv[NH][kMaxGpw];
+        // the scale words first (a few bytes; they land with the activations),
+        // then the weights in group order, so that each group's products and
+        // fold start as soon as its own weights land
         uint32_t sv[NH][kMaxGpw / 4];
+#pragma unroll
+        for (int i = 0; i < kMaxGpw / 4; ++i) {  // group 4 i + q
+            const int gi = 4 * i + q < NG ? 4 * i + q : NG - 1;
+#pragma unroll
+            for (int h = 0; h < NH; ++h) sv[h][i] = a.ws[(row + h * N) * NG + gi];
+        }
+        uint4 wv[NH][kMaxGpw];
 #pragma unroll
         for (int i = 0; i < kMaxGpw; ++i) {
             const int gi = i < NG ? i : NG - 1;
@@ -346,35 +362,11 @@ __global__ __launch_bounds__(64 * kRowsWaves) void gemv_mfma_rows_kernel(MfmaGem
                 wv[h][i] = load16(reinterpret_cast<const unsigned char*>(a.wq) + (row + h * N) * (K / 2) +
                                   64 * gi + 16 * q);
         }
-#pragma unroll
-        for (int i = 0; i < kMaxGpw / 4; ++i) {  // group 4 i + q
-            const int gi = 4 * i + q < NG ? 4 * i + q : NG - 1;
-#pragma unroll
-            for (int h = 0; h < NH; ++h) sv[h][i] = a.ws[(row + h * N) * NG + gi];
-        }
-        // the direct-to-LDS loads (issued first) have landed: at most the
-        // weight loads remain in flight
-        constexpr int kLoads = NH * (kMaxGpw + kMaxGpw / 4);
+        // the direct-to-LDS loads and the scale words (issued first) have
+        // landed: at most the weight loads remain in flight
+        constexpr int kLoads = NH * kMaxGpw;
         static_assert(kLoads < 64, "vmcnt range");
         __builtin_amdgcn_s_waitcnt((kLoads & 15) | ((kLoads >> 4) << 14) | (7 << 4));
-        asm volatile("s_barrier" ::: "memory");
-        // two MFMAs per group (codes 32 q .. +15, then +16 .. +31)
-        v4i dres[NH][kMaxGpw];
-#pragma unroll
-        for (int i = 0; i < kMaxGpw; ++i) {
-            if (i >= NG) continue;
-            const v4i a0 = *reinterpret_cast<const v4i*>(xr + 128 * i);
-            const v4i a1 = *reinterpret_cast<const v4i*>(xr + 128 * i + 16);
-#pragma unroll
-            for (int h = 0; h < NH; ++h) {
-                const v4i b0{(int)(wv[h][i].x & kNibbleMask), (int)((wv[h][i].x >> 4) & kNibbleMask),
-                             (int)(wv[h][i].y & kNibbleMask), (int)((wv[h][i].y >> 4) & kNibbleMask)};
-                const v4i b1{(int)(wv[h][i].z & kNibbleMask), (int)((wv[h][i].z >> 4) & kNibbleMask),
-                             (int)(wv[h][i].w & kNibbleMask), (int)((wv[h][i].w >> 4) & kNibbleMask)};
-                v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, v4i{0, 0, 0, 0}, 0, 0, 0);
-                dres[h][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, d, 0, 0, 0);
-            }
-        }
         // every lane needs the (s, m) of all groups of its row: through LDS
 #pragma unroll
         for (int i = 0; i < kMaxGpw / 4; ++i) {
@@ -385,48 +377,55 @@ __global__ __launch_bounds__(64 * kRowsWaves) void gemv_mfma_rows_kernel(MfmaGem
                     sm_lds[(h * RB + 16 * wave + c) * NGP + gi] = make_float2(f16lo(sv[h][i]), f16hi(sv[h][i]));
             }
         }
-        __syncthreads();
-        // fp32 fold of (token 4 q + j, row): a chain per pair of groups
-        // (those that exist), the pairwise tree over the 8 pairs
-        float v[NH][4];
+        __syncthreads();  // the activations (every wave's loads) and the (s, m) pairs
+        // per group, in order: two MFMAs (codes 32 q .. +15, then +16 .. +31)
+        // and at once the fp32 fold of (token 4 q + j, row) -- a chain per
+        // pair of groups (those that exist); the pairwise tree over the 8
+        // pairs follows
+        const int rows_total = NH * (int)N;
+        float cc[NH][4][8];
 #pragma unroll
-        for (int h = 0; h < NH; ++h) {
-            float cc[4][8];
+        for (int h = 0; h < NH; ++h)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int k = 0; k < 8; ++k) cc[j][k] = 0.0f;
+                for (int k = 0; k < 8; ++k) cc[h][j][k] = 0.0f;
 #pragma unroll
-            for (int i = 0; i < kMaxGpw; ++i) {
-                if (i < NG) {  // uniform
-                    const float2 w = sm_lds[(h * RB + 16 * wave + c) * NGP + i];
+        for (int i = 0; i < kMaxGpw; ++i) {
+            if (i >= NG) continue;  // uniform
+            const v4i a0 = *reinterpret_cast<const v4i*>(xr + 128 * i);
+            const v4i a1 = *reinterpret_cast<const v4i*>(xr + 128 * i + 16);
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const v4i b0{(int)(wv[h][i].x & kNibbleMask), (int)((wv[h][i].x >> 4) & kNibbleMask),
+                             (int)(wv[h][i].y & kNibbleMask), (int)((wv[h][i].y >> 4) & kNibbleMask)};
+                const v4i b1{(int)(wv[h][i].z & kNibbleMask), (int)((wv[h][i].z >> 4) & kNibbleMask),
+                             (int)(wv[h][i].w & kNibbleMask), (int)((wv[h][i].w >> 4) & kNibbleMask)};
+                v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, v4i{0, 0, 0, 0}, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, d, 0, 0, 0);
+                const float2 w = sm_lds[(h * RB + 16 * wave + c) * NGP + i];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
+                    cc[h][j][i / 2] = fmaf(w.y, (float)xs_lds[t * NG + i], fmaf(w.x, (float)d[j], cc[h][j][i / 2]));
+                }
+                if (a.acc_dump) {  // test hook: the group sums the chains fold
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
-                        cc[j][i / 2] = fmaf(w.y, (float)xs_lds[t * NG + i],
-                                            fmaf(w.x, (float)dres[h][i][j], cc[j][i / 2]));
+                        const int t = 4 * q + j;
+                        if (t < a.M && rr < N) a.acc_dump[((int64_t)t * rows_total + h * N + rr) * NG + i] = d[j];
                     }
                 }
             }
+        }
+        float v[NH][4];
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
-                v[h][j] = tree8(cc[j]) * dx_lds[t];
+                v[h][j] = tree8(cc[h][j]) * dx_lds[t];
             }
-        }
-        if (a.acc_dump) {  // test hook: the group sums the chains folded
-            const int rows_total = NH * (int)N;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int t = 4 * q + j;
-                if (t < a.M && rr < N)
-#pragma unroll
-                    for (int h = 0; h < NH; ++h)
-#pragma unroll
-                        for (int i = 0; i < kMaxGpw; ++i)  // constant indices: registers
-                            if (i < NG) a.acc_dump[((int64_t)t * rows_total + h * N + rr) * NG + i] = dres[h][i][j];
-            }
-        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int t = 4 * q + j;
