@@ -300,8 +300,11 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
 // repeating tokens 0..7, odd pairs in the upper lanes, a lane exchange
 // before the tree) was measured much slower (38.9 -> 63.3 us at 8 tokens x
 // 151,936 rows) and is not used.
+// Store and argmax instances are held to 96 VGPRs: five workgroups per CU
+// (the LDS allows five) overlap one another's loads and compute (38.65
+// against 39.86 us at 8 tokens x 151,936 rows; six spill).
 template <int MT, int MODE, bool ARGMAX>
-__global__ __launch_bounds__(64 * kRowsWaves) void gemv_mfma_rows_kernel(MfmaGemvParams p) {
+__global__ __launch_bounds__(64 * kRowsWaves, (MODE == 0 ? 5 : 1)) void gemv_mfma_rows_kernel(MfmaGemvParams p) {
     constexpr int NH = MODE == 2 ? 2 : 1;
     constexpr int RB = 16 * kRowsWaves;  // rows per workgroup: one 16-row block per wave
     constexpr int NT = 64 * kRowsWaves;  // threads
