@@ -815,6 +815,11 @@ Plan make_plan(const LinearArgs& a, bool argmax, bool qin = false) {
         if (grid_of(c) <= target) { ipw = c; break; }
     }
     if (ipw == 1 && grid_of(2) >= kGemvCus) ipw = 2;
+    // The fused lm_head argmax: three rows per wave while that keeps the grid
+    // within 8,192 workgroups (one token: 10.65 against 11.24 us at 32,768
+    // rows, where the target rule gave eight; at 151,936 rows three and eight
+    // are alike and the rule's eight keeps the grid at 4,748).
+    if (argmax && grid_of(3) <= 8192) ipw = 3;
     // LDS budget: 64 KiB per workgroup
     auto lds_of = [&](int ipw_) {
         size_t rb = (size_t)p.nslots * ipw_;
