@@ -41,6 +41,7 @@ constexpr int kBK = 128;          // codes per K step (= bytes per int8 tile row
 constexpr int kBM = 128;          // tokens per tile
 constexpr int kWaveGroup = 256;   // 4 waves: 2 along M x 2 along N
 constexpr int kXcds = 8;          // MI355X: 8 XCDs, workgroups dispatched round robin
+constexpr int kLdsBytes = 160 * 1024;  // LDS per workgroup (gfx950)
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -151,9 +152,16 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     constexpr int TR_STRIDE = 36;  // floats per row of a wave's 32 x 32 output transpose (16-byte rows)
     constexpr int TR_SZ = NWAVES * 32 * TR_STRIDE * 4;
     constexpr int BODY_SZ = NST * ST_SZ > RED_SZ ? NST * ST_SZ : RED_SZ;
-    constexpr int LDS_SZ = (BODY_SZ > TR_SZ ? BODY_SZ : TR_SZ) + BM * 4;  // + the tile's per-token scales
+    // + the tile's per-token scales; then (per-token group-128 format) the
+    // tile's scale words for the whole K range, loaded once: BN rows of NGP
+    // words (NGP = NG rounded up to odd, so that 32 consecutive rows read
+    // distinct banks), in what is left of the 160 KiB
+    constexpr int SP_BASE = (BODY_SZ > TR_SZ ? BODY_SZ : TR_SZ) + BM * 4;
+    constexpr int SP_NGP = FAST ? (kLdsBytes - SP_BASE) / (BN * 4) : 0;  // row words that fit
+    constexpr int LDS_SZ = SP_BASE + BN * SP_NGP * 4;
+    static_assert(LDS_SZ <= kLdsBytes, "LDS");
     __shared__ __align__(1024) unsigned char lds[LDS_SZ];
-    float* dx_tile = reinterpret_cast<float*>(lds + LDS_SZ - BM * 4);
+    float* dx_tile = reinterpret_cast<float*>(lds + SP_BASE - BM * 4);
     auto As = [&](int st) -> int8_t* { return reinterpret_cast<int8_t*>(lds + st * ST_SZ); };
     auto Bs = [&](int st) -> uint32_t* { return reinterpret_cast<uint32_t*>(lds + st * ST_SZ + A_SZ); };
     auto Ss = [&](int st) -> uint32_t* { return reinterpret_cast<uint32_t*>(lds + st * ST_SZ + A_SZ + B_SZ); };
@@ -247,8 +255,17 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
         const int w = 64 * (D_PW * wave + i) + lane;
         d_off[i] = (uint32_t)(trow(w % BM) * (K / 32) + w / BM);
     }
+    // The scale words of every K step at once when they fit (the per-token
+    // group-128 format) and the row has 32 steps or more: each step
+    // otherwise fetches BN scattered 4-byte words, one cache-line request
+    // each.  Measured: K = 6144, N = 2048 27.08 -> 25.49 us; at K = 2048 (16
+    // steps) the preload's start-up cost outweighs it, 22.31 -> 22.65 us.
+    const int NGPs = NG + 1 - (NG & 1);  // odd row stride
+    // (the last 64-word instruction may run up to 63 words past BN rows)
+    const bool spre = FAST && nsteps >= 32 && BN * NGPs + 64 <= BN * SP_NGP;  // uniform
+    const uint32_t* sp_lds = reinterpret_cast<const uint32_t*>(lds + SP_BASE);
     // Every load is unconditional (steps past the end re-read the last one),
-    // so each call issues exactly VM vector-memory instructions per wave.
+    // so each call issues the same vector-memory instructions per wave.
     // LDS byte address of the ring (scalar); stage st, part at byte b of it
     const uint32_t lds0 = lds_addr(lds);
     auto stage_at = [&](int st, int b) -> uint32_t { return lds0 + (uint32_t)(st * ST_SZ + b); };
@@ -261,8 +278,11 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
         for (int i = 0; i < A_PW; ++i) dma16_at(xq, a_off[i], stage_at(st, 1024 * (A_PW * wave + i)));
 #pragma unroll
         for (int i = 0; i < B_PW; ++i) dma16_at(wq, b_off[i], stage_at(st, A_SZ + 1024 * (B_PW * wave + i)));
+        if (!spre) {
 #pragma unroll
-        for (int i = 0; i < S_PW; ++i) dma4_at(ws, 4 * s_off[i], stage_at(st, A_SZ + B_SZ + 256 * (S_PW * wave + i)));
+            for (int i = 0; i < S_PW; ++i)
+                dma4_at(ws, 4 * s_off[i], stage_at(st, A_SZ + B_SZ + 256 * (S_PW * wave + i)));
+        }
         if constexpr (!FAST) {
             const int32_t* xs = a.xs + step * NES;
 #pragma unroll
@@ -277,6 +297,16 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
         }
     };
 
+    if (spre) {  // 64 words per instruction, the workgroup's waves in turn
+        const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int nins = (BN * NGPs + 63) / 64;
+        for (int i = wid; i < nins; i += NWAVES) {
+            const int pw = 64 * i + lane;
+            const int r = pw / NGPs, gg = pw - r * NGPs;
+            const uint32_t src = r < BN && gg < NG ? (uint32_t)(wrow(r) * NG + gg) : 0u;  // padding: word 0
+            dma4_at(a.ws, 4 * src, lds0 + (uint32_t)(SP_BASE + 256 * i));
+        }
+    }
     // the tile's per-token scales for the epilogue, ahead of the ring loads
     // (every wait below also covers them)
     if (PT && wave < BM / 64 && (KS == 1 || wk == 0))
@@ -403,6 +433,9 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
         const int8_t* Ab = As(st);
         const uint8_t* Bb = reinterpret_cast<const uint8_t*>(Bs(st));
         const uint32_t* Sb = Ss(st);
+        // (FAST) scale word of tile row br for this step: Sx[br * sst]
+        const uint32_t* Sx = spre ? sp_lds + step : Sb;
+        const int sst = spre ? NGPs : 1;
         if (FAST) {
             // k-slice ks of lane half h = codes 64 h + 16 ks .. +15 of the
             // group (any assignment shared by both operands gives the same
@@ -427,7 +460,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
                     const int br = bcol(j);
                     pb[j][0] = *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * ((2 * h) ^ swz_b(br)));
                     pb[j][1] = *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * ((2 * h + 1) ^ swz_b(br)));
-                    sv[j] = f16lo(Sb[br]);
+                    sv[j] = f16lo(Sx[br * sst]);
                 }
             }
 #pragma unroll
@@ -450,7 +483,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
                     for (int i = 0; i < TM; ++i)
                         acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks], ks == 0 ? v16i{} : acc[i],
                                                                        0, 0, 0);
-                const float s = PRE ? sv[PRE ? j : 0] : f16lo(Sb[br]);
+                const float s = PRE ? sv[PRE ? j : 0] : f16lo(Sx[br * sst]);
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
                     if (DUMP) dump(step, 0, i, br, acc[i]);
