@@ -263,6 +263,7 @@ GEMM_CASES = [
     (200, 2048, 320, 128, None, 2),   # mode 2 at width 256
     (129, 1024, 130, 32, None, 0),
     (300, 6144, 2048, 128, None, 1),  # down-projection shape, tile width 64
+    (64, 4096, 256, 128, None, 2),    # 32 steps: scale words preloaded, gate/up pairs
 ]
 
 
