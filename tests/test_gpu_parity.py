@@ -264,6 +264,8 @@ GEMM_CASES = [
     (129, 1024, 130, 32, None, 0),
     (300, 6144, 2048, 128, None, 1),  # down-projection shape, tile width 64
     (64, 4096, 256, 128, None, 2),    # 32 steps: scale words preloaded, gate/up pairs
+    (70, 3072, 192, 128, None, 0),    # 3 min-term blocks over two wave groups
+    (40, 2176, 130, 128, None, 1),    # 17 groups: min-term blocks word by word
 ]
 
 
@@ -299,6 +301,7 @@ def test_gemm_bit_exact(M, K, N, G, GA, mode):
 # 256 (mode 2), 64; the other formats at width 128
 WIDE_CASES = [
     (2048, 6144, 128, None, 0),
+    (4096, 6144, 128, None, 0),   # tile width 192, min-term blocks reloaded
     (2048, 8192, 128, None, 0),
     (2048, 4096, 128, None, 0),
     (2048, 4096, 128, None, 2),

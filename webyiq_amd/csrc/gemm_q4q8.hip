@@ -58,6 +58,11 @@ struct GemmParams {
 // rows 64 bytes (4 chunks); chunk c of row r sits at position c ^ f(r).
 __device__ __forceinline__ int swz_a(int r) { return (r ^ (r >> 3)) & 7; }
 __device__ __forceinline__ int swz_b(int r) { return (r >> 1) & 3; }
+// Packed weight rows of two K steps (128 bytes, 8 chunks: the even step's 4,
+// then the odd step's): chunk c of row r at position c ^ swz_p(r), so that 16
+// consecutive rows' 16-byte reads of one chunk cover 256 distinct bytes of
+// banks.
+__device__ __forceinline__ int swz_p(int r) { return (r >> 1) & 7; }
 
 // 16 codes (8 packed bytes) -> 16 int8 in code order: the low nibbles of a
 // word are codes 8i..8i+3, the high nibbles 8i+4..8i+7.
@@ -143,15 +148,22 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
 
     // LDS: NST stages of (activations, packed weights, scale words, group
     // sums, per-32 scales); the partial sums of the second wave group reuse
-    // it at the end
+    // it at the end.  With two wave groups (PAIRB) the packed weights of a
+    // round's two steps share one buffer of BN rows x 128 bytes, NST / 2 of
+    // them after the stages: a row's two 64-byte halves are one cache line,
+    // fetched by one load, half of the rows by each group.
+    constexpr bool PAIRB = KS == 2;
     constexpr int A_SZ = BM * kBK, B_SZ = BN * kBK / 2, S_SZ = S_PW * 1024;
     constexpr int X_SZ = FAST ? 16 : NES * BM * 4, D_SZ = PT ? 16 : NES * BM * 4;
-    constexpr int ST_SZ = A_SZ + B_SZ + S_SZ + X_SZ + D_SZ;
+    constexpr int OFF_S = A_SZ + (PAIRB ? 0 : B_SZ), OFF_X = OFF_S + S_SZ, OFF_D = OFF_X + X_SZ;
+    constexpr int ST_SZ = OFF_D + D_SZ;
+    constexpr int PB_BASE = NST * ST_SZ;  // pair buffers (PAIRB)
+    constexpr int RING_SZ = PB_BASE + (PAIRB ? NST * B_SZ : 0);
     constexpr int RED_SZ = KS > 1 ? kWaveGroup * TM * TN * 16 * 4 : 0;
     constexpr int NWAVES = gemm_threads(G, PT) / 64;
     constexpr int TR_STRIDE = 36;  // floats per row of a wave's 32 x 32 output transpose (16-byte rows)
     constexpr int TR_SZ = NWAVES * 32 * TR_STRIDE * 4;
-    constexpr int BODY_SZ = NST * ST_SZ > RED_SZ ? NST * ST_SZ : RED_SZ;
+    constexpr int BODY_SZ = RING_SZ > RED_SZ ? RING_SZ : RED_SZ;
     // + the tile's per-token scales; then (per-token group-128 format) the
     // tile's scale words for the whole K range, loaded once: BN rows of NGP
     // words (NGP = NG rounded up to odd, so that 32 consecutive rows read
@@ -163,14 +175,16 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     __shared__ __align__(1024) unsigned char lds[LDS_SZ];
     float* dx_tile = reinterpret_cast<float*>(lds + SP_BASE - BM * 4);
     auto As = [&](int st) -> int8_t* { return reinterpret_cast<int8_t*>(lds + st * ST_SZ); };
-    auto Bs = [&](int st) -> uint32_t* { return reinterpret_cast<uint32_t*>(lds + st * ST_SZ + A_SZ); };
-    auto Ss = [&](int st) -> uint32_t* { return reinterpret_cast<uint32_t*>(lds + st * ST_SZ + A_SZ + B_SZ); };
+    // packed weights of stage st: its own region, or (PAIRB) the pair buffer
+    // of its round, the step's half selected when reading
+    auto Bs = [&](int st) -> uint32_t* {
+        return reinterpret_cast<uint32_t*>(PAIRB ? lds + PB_BASE + (st >> 1) * 2 * B_SZ : lds + st * ST_SZ + A_SZ);
+    };
+    auto Ss = [&](int st) -> uint32_t* { return reinterpret_cast<uint32_t*>(lds + st * ST_SZ + OFF_S); };
     auto Xs = [&](int st) -> int32_t* {  // [group][token]
-        return reinterpret_cast<int32_t*>(lds + st * ST_SZ + A_SZ + B_SZ + S_SZ);
+        return reinterpret_cast<int32_t*>(lds + st * ST_SZ + OFF_X);
     };
-    auto Ds = [&](int st) -> float* {
-        return reinterpret_cast<float*>(lds + st * ST_SZ + A_SZ + B_SZ + S_SZ + X_SZ);
-    };
+    auto Ds = [&](int st) -> float* { return reinterpret_cast<float*>(lds + st * ST_SZ + OFF_D); };
 
     const LinearArgs& a = p.a;
     pin_arg(a.wq); pin_arg(a.ws); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs); pin_arg(a.y);
@@ -235,9 +249,14 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
         a_off[i] = (uint32_t)(trow(r) * K + 16 * ((lane % 8) ^ swz_a(r)));
     }
 #pragma unroll
-    for (int i = 0; i < B_PW; ++i) {  // block = 16 rows of 64 B
-        const int r = 16 * (B_PW * wave + i) + lane / 4;
-        b_off[i] = (uint32_t)(wrow(r) * (K / 2) + 16 * ((lane % 4) ^ swz_b(r)));
+    for (int i = 0; i < B_PW; ++i) {
+        if constexpr (PAIRB) {  // block = 8 rows of 128 B; the 8 waves cover BN rows
+            const int r = 8 * ((4 * wk + wave) * B_PW + i) + lane / 8;
+            b_off[i] = (uint32_t)(wrow(r) * (K / 2) + 16 * ((lane % 8) ^ swz_p(r)));
+        } else {  // block = 16 rows of 64 B
+            const int r = 16 * (B_PW * wave + i) + lane / 4;
+            b_off[i] = (uint32_t)(wrow(r) * (K / 2) + 16 * ((lane % 4) ^ swz_b(r)));
+        }
     }
 #pragma unroll
     for (int i = 0; i < S_PW; ++i) {  // block = 64 scale words, [row][group]
@@ -272,30 +291,125 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     auto dma = [&](int step, const int st) {
         step = step < nsteps ? step : nsteps - 1;
         const int8_t* xq = a.xq + step * kBK;
-        const uint8_t* wq = reinterpret_cast<const uint8_t*>(a.wq) + step * (kBK / 2);
         const uint32_t* ws = a.ws + step * NGS;
 #pragma unroll
         for (int i = 0; i < A_PW; ++i) dma16_at(xq, a_off[i], stage_at(st, 1024 * (A_PW * wave + i)));
+        if constexpr (PAIRB) {
+            // steps s0 and s0 + 1 into the pair buffer of stage st; with an
+            // odd step count the last round has no second step, and the lanes
+            // of the second halves re-read the first (a row's end is not
+            // passed): the half of a lane's chunk is bit 2 of
+            // (lane % 8) ^ swz_p(r), = ((lane >> 2) ^ block) & 1
+            const int s0 = step & ~1;
+            const uint8_t* wq = reinterpret_cast<const uint8_t*>(a.wq) + s0 * (kBK / 2);
+            const bool tail = s0 + 1 >= nsteps;  // uniform
 #pragma unroll
-        for (int i = 0; i < B_PW; ++i) dma16_at(wq, b_off[i], stage_at(st, A_SZ + 1024 * (B_PW * wave + i)));
+            for (int i = 0; i < B_PW; ++i) {
+                const int blk = (4 * wk + wave) * B_PW + i;
+                const uint32_t off = tail ? b_off[i] - 64u * (uint32_t)(((lane >> 2) ^ blk) & 1) : b_off[i];
+                dma16_at(wq, off, lds0 + (uint32_t)(PB_BASE + (st >> 1) * 2 * B_SZ + 1024 * blk));
+            }
+        } else {
+            const uint8_t* wq = reinterpret_cast<const uint8_t*>(a.wq) + step * (kBK / 2);
+#pragma unroll
+            for (int i = 0; i < B_PW; ++i) dma16_at(wq, b_off[i], stage_at(st, A_SZ + 1024 * (B_PW * wave + i)));
+        }
         if (!spre) {
 #pragma unroll
             for (int i = 0; i < S_PW; ++i)
-                dma4_at(ws, 4 * s_off[i], stage_at(st, A_SZ + B_SZ + 256 * (S_PW * wave + i)));
+                dma4_at(ws, 4 * s_off[i], stage_at(st, OFF_S + 256 * (S_PW * wave + i)));
         }
         if constexpr (!FAST) {
             const int32_t* xs = a.xs + step * NES;
 #pragma unroll
             for (int i = 0; i < X_PW; ++i)
-                dma4_at(xs, 4 * x_off[i], stage_at(st, A_SZ + B_SZ + S_SZ + 256 * (X_PW * wave + i)));
+                dma4_at(xs, 4 * x_off[i], stage_at(st, OFF_X + 256 * (X_PW * wave + i)));
         }
         if constexpr (!PT) {
             const float* dxp = a.dx + step * NES;
 #pragma unroll
             for (int i = 0; i < D_PW; ++i)
-                dma4_at(dxp, 4 * d_off[i], stage_at(st, A_SZ + B_SZ + S_SZ + X_SZ + 256 * (D_PW * wave + i)));
+                dma4_at(dxp, 4 * d_off[i], stage_at(st, OFF_D + 256 * (D_PW * wave + i)));
         }
     };
+
+    // ---------------- compute layout ----------------
+    const int wm = wave >> 1, wn = wave & 1;
+    const int l32 = lane & 31, h = lane >> 5;
+    // tile row (of W) of this lane's column in subtile j
+    auto bcol = [&](int j) -> int {
+        if (MODE == 2) {
+            constexpr int H = TN / 2;
+            return (j < H ? wn * (BN / 4) + 32 * j : BN / 2 + wn * (BN / 4) + 32 * (j - H)) + l32;
+        }
+        return wn * (BN / 2) + 32 * j + l32;
+    };
+    // token row (within the tile) of accumulator element r of subtile i
+    auto arow = [&](int i, int r) -> int { return wm * 64 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3); };
+
+    // min term operands: blocks of 8 groups, wave group wk taking blocks
+    // wk, wk + KS, ... (the groups' partial sums are added at the end like
+    // their K steps'), with NSL blocks in flight per wave in registers: two
+    // up to 2 columns per wave, one at 3.  The first NSL are requested
+    // before any tile load: loads return in issue order, so operands
+    // requested after the tiles would land after them.  With 4 columns the
+    // registers are short: wave group 0 loads each block after the tiles,
+    // when it is used.
+    constexpr int NSL = TN <= 2 ? 2 : TN == 3 ? 1 : 0;
+    constexpr int NSA = NSL > 0 ? NSL : 1;  // register slots
+    const int nfull = NG % 8 == 0 ? NG / 8 : 0;  // full blocks (32-byte aligned rows: K a multiple of 1024)
+    const int nblk = (NG + 7) / 8;
+    const int32_t* xr[TM];
+    const uint32_t* sr[TN];
+    int32_t xv[NSA][TM][8];
+    uint32_t wv[NSA][TN][8];
+    auto mt_full = [&](int32_t (&x)[TM][8], uint32_t (&w)[TN][8], int blk) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int4 lo = *reinterpret_cast<const int4*>(xr[i] + 8 * blk);
+            const int4 hi = *reinterpret_cast<const int4*>(xr[i] + 8 * blk + 4);
+            x[i][0] = lo.x; x[i][1] = lo.y; x[i][2] = lo.z; x[i][3] = lo.w;
+            x[i][4] = hi.x; x[i][5] = hi.y; x[i][6] = hi.z; x[i][7] = hi.w;
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const uint4 lo = *reinterpret_cast<const uint4*>(sr[j] + 8 * blk);
+            const uint4 hi = *reinterpret_cast<const uint4*>(sr[j] + 8 * blk + 4);
+            w[j][0] = lo.x; w[j][1] = lo.y; w[j][2] = lo.z; w[j][3] = lo.w;
+            w[j][4] = hi.x; w[j][5] = hi.y; w[j][6] = hi.z; w[j][7] = hi.w;
+        }
+    };
+    // word by word, indices past the last group clamped (their values are zeroed)
+    auto mt_words = [&](int32_t (&x)[TM][8], uint32_t (&w)[TN][8], int blk) {
+        const int b = 8 * blk;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) x[i][u] = xr[i][b + u < NG ? b + u : NG - 1];
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) w[j][u] = sr[j][b + u < NG ? b + u : NG - 1];
+    };
+    auto mt_load = [&](auto slot, int blk) {
+        constexpr int S = decltype(slot)::value;
+        if (blk < nfull) mt_full(xv[S], wv[S], blk);
+        else mt_words(xv[S], wv[S], blk);
+    };
+    using ic0 = std::integral_constant<int, 0>;
+    using ic1 = std::integral_constant<int, NSA - 1>;
+    auto mt_rows = [&]() {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) xr[i] = a.xs + trow(wm * 64 + 32 * i + l32) * NE;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) sr[j] = a.ws + wrow(bcol(j)) * NG;
+    };
+    if constexpr (FAST && NSL >= 1) {
+        mt_rows();
+        if (wk < nblk) mt_load(ic0{}, wk);
+        if constexpr (NSL == 2)
+            if (wk + KS < nblk) mt_load(ic1{}, wk + KS);
+    }
 
     if (spre) {  // 64 words per instruction, the workgroup's waves in turn
         const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -320,20 +434,6 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     } else {
         dma(wk, wk);
     }
-
-    // ---------------- compute layout ----------------
-    const int wm = wave >> 1, wn = wave & 1;
-    const int l32 = lane & 31, h = lane >> 5;
-    // tile row (of W) of this lane's column in subtile j
-    auto bcol = [&](int j) -> int {
-        if (MODE == 2) {
-            constexpr int H = TN / 2;
-            return (j < H ? wn * (BN / 4) + 32 * j : BN / 2 + wn * (BN / 4) + 32 * (j - H)) + l32;
-        }
-        return wn * (BN / 2) + 32 * j + l32;
-    };
-    // token row (within the tile) of accumulator element r of subtile i
-    auto arow = [&](int i, int r) -> int { return wm * 64 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3); };
 
     v16f facc[TM][TN];
 #pragma unroll
@@ -366,53 +466,37 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
             for (int j = 0; j < TN; ++j)
                 facc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[i], mb[j], facc[i][j], 0, 0, 0);
     };
-    auto min_term = [&]() {
-        const int32_t* xr[TM];
-        const uint32_t* sr[TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i) xr[i] = a.xs + trow(wm * 64 + 32 * i + l32) * NE;
-#pragma unroll
-        for (int j = 0; j < TN; ++j) sr[j] = a.ws + wrow(bcol(j)) * NG;
-        // full blocks: rows are 32-byte aligned when the group count is a
-        // multiple of 8 (K a multiple of 1024)
-        const int nfull = NG % 8 == 0 ? NG / 8 : 0;
-        for (int blk = 0; blk < nfull; ++blk) {
-            int32_t xv[TM][8];
-            uint32_t wv[TN][8];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                const int4 lo = *reinterpret_cast<const int4*>(xr[i] + 8 * blk);
-                const int4 hi = *reinterpret_cast<const int4*>(xr[i] + 8 * blk + 4);
-                xv[i][0] = lo.x; xv[i][1] = lo.y; xv[i][2] = lo.z; xv[i][3] = lo.w;
-                xv[i][4] = hi.x; xv[i][5] = hi.y; xv[i][6] = hi.z; xv[i][7] = hi.w;
+    // this wave group's min term blocks, the two register slots in turn
+    if constexpr (FAST && NSL == 0) {  // wave group 0 alone, block by block
+        if (wk == 0) {
+            mt_rows();
+            for (int blk = 0; blk < nfull; ++blk) {
+                int32_t x[TM][8];
+                uint32_t w[TN][8];
+                mt_full(x, w, blk);
+                min_term_block(x, w, 8 * blk);
             }
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const uint4 lo = *reinterpret_cast<const uint4*>(sr[j] + 8 * blk);
-                const uint4 hi = *reinterpret_cast<const uint4*>(sr[j] + 8 * blk + 4);
-                wv[j][0] = lo.x; wv[j][1] = lo.y; wv[j][2] = lo.z; wv[j][3] = lo.w;
-                wv[j][4] = hi.x; wv[j][5] = hi.y; wv[j][6] = hi.z; wv[j][7] = hi.w;
+            for (int blk = nfull; blk < nblk; ++blk) {
+                int32_t x[TM][8];
+                uint32_t w[TN][8];
+                mt_words(x, w, blk);
+                min_term_block(x, w, 8 * blk);
             }
-            min_term_block(xv, wv, 8 * blk);
         }
-        // otherwise word by word, indices past the last group clamped and
-        // their values zeroed
-        for (int b = 8 * nfull; b < NG; b += 8) {
-            int32_t xv[TM][8];
-            uint32_t wv[TN][8];
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int u = 0; u < 8; ++u) xv[i][u] = xr[i][b + u < NG ? b + u : NG - 1];
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-#pragma unroll
-                for (int u = 0; u < 8; ++u) wv[j][u] = sr[j][b + u < NG ? b + u : NG - 1];
-            min_term_block(xv, wv, b);
+    } else if constexpr (FAST && NSL == 1) {
+        for (int blk = wk; blk < nblk; blk += KS) {
+            min_term_block(xv[0], wv[0], 8 * blk);
+            if (blk + KS < nblk) mt_load(ic0{}, blk + KS);
         }
-    };
-    // the min term is added once, by wave group 0
-    if (FAST && wk == 0) min_term();
+    } else if constexpr (FAST) {
+        for (int blk = wk; blk < nblk; blk += 2 * KS) {
+            min_term_block(xv[0], wv[0], 8 * blk);
+            if (blk + 2 * KS < nblk) mt_load(ic0{}, blk + 2 * KS);
+            if (blk + KS >= nblk) break;
+            min_term_block(xv[NSA - 1], wv[NSA - 1], 8 * (blk + KS));
+            if (blk + 3 * KS < nblk) mt_load(ic1{}, blk + 3 * KS);
+        }
+    }
 
     // the first step of each group has landed
     step_barrier<KS == 1 ? (NST - 2) * VM : 0>();
@@ -432,6 +516,13 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     auto compute = [&](const int step, const int st) {
         const int8_t* Ab = As(st);
         const uint8_t* Bb = reinterpret_cast<const uint8_t*>(Bs(st));
+        // 16-byte chunk c (of 4) of this step's packed weights in tile row br
+        auto bfrag = [&](int br, int c) -> uint4 {
+            if constexpr (PAIRB)
+                return *reinterpret_cast<const uint4*>(Bb + br * 128 + 16 * ((4 * (st & 1) + c) ^ swz_p(br)));
+            else
+                return *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * (c ^ swz_b(br)));
+        };
         const uint32_t* Sb = Ss(st);
         // (FAST) scale word of tile row br for this step: Sx[br * sst]
         const uint32_t* Sx = spre ? sp_lds + step : Sb;
@@ -458,8 +549,8 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
                     const int br = bcol(j);
-                    pb[j][0] = *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * ((2 * h) ^ swz_b(br)));
-                    pb[j][1] = *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * ((2 * h + 1) ^ swz_b(br)));
+                    pb[j][0] = bfrag(br, 2 * h);
+                    pb[j][1] = bfrag(br, 2 * h + 1);
                     sv[j] = f16lo(Sx[br * sst]);
                 }
             }
@@ -471,8 +562,8 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
                     p0 = pb[j][0];
                     p1 = pb[j][1];
                 } else {
-                    p0 = *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * ((2 * h) ^ swz_b(br)));
-                    p1 = *reinterpret_cast<const uint4*>(Bb + br * 64 + 16 * ((2 * h + 1) ^ swz_b(br)));
+                    p0 = bfrag(br, 2 * h);
+                    p1 = bfrag(br, 2 * h + 1);
                 }
                 const v4i bf[4] = {expand8(p0.x, p0.y), expand8(p0.z, p0.w), expand8(p1.x, p1.y),
                                    expand8(p1.z, p1.w)};
@@ -586,27 +677,36 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
 
     // subtiles this wave stores: all of them with one wave group; with two,
     // group g stores subtile row i = g after adding the other group's partial
-    // sums (exchanged through LDS, lane-major; the fp32 addition of two
-    // partials is the same in either order)
+    // sums (exchanged through LDS, 16 bytes per lane and instruction,
+    // lane-major; the fp32 addition of two partials is the same in either
+    // order)
     constexpr int I0 = 0, I1 = KS > 1 ? 1 : TM;
     int ilo = I0, ihi = I1;
     if constexpr (KS > 1) {
         static_assert(TM == 2, "one subtile row per wave group");
-        float* red = reinterpret_cast<float*>(lds);
+        v4f* red = reinterpret_cast<v4f*>(lds);
         const int give = 1 - wk;  // the subtile row the other group stores
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                red[(((give * 4 + wave) * TN + j) * 16 + r) * 64 + lane] = wk == 0 ? facc[1][j][r] : facc[0][j][r];
+            for (int q = 0; q < 4; ++q) {
+                v4f v;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = wk == 0 ? facc[1][j][4 * q + u] : facc[0][j][4 * q + u];
+                red[(((give * 4 + wave) * TN + j) * 4 + q) * 64 + lane] = v;
+            }
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float o = red[(((wk * 4 + wave) * TN + j) * 16 + r) * 64 + lane];
-                if (wk == 0) facc[0][j][r] = facc[0][j][r] + o;
-                else facc[1][j][r] = o + facc[1][j][r];
+            for (int q = 0; q < 4; ++q) {
+                const v4f o = red[(((wk * 4 + wave) * TN + j) * 4 + q) * 64 + lane];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int r = 4 * q + u;
+                    if (wk == 0) facc[0][j][r] = facc[0][j][r] + o[u];
+                    else facc[1][j][r] = o[u] + facc[1][j][r];
+                }
             }
         ilo = wk;
         ihi = wk + 1;
