@@ -373,8 +373,9 @@ def copies_for(nbytes, budget=512 << 20, cap=1024):
 
 def bench_configs(torch, lib, ops):
     """BASELINE configs 2, 3 and 5 (decode MLP block, M<=8 verify shapes,
-    lm_head + argmax): us per launch (graph replays over weight copies, so
-    weights stream from HBM) and algorithmic GB/s."""
+    lm_head + argmax) and one GPU's share of them when split over 2-8 GPUs:
+    us per launch (graph replays over weight copies, so weights stream from
+    HBM) and algorithmic GB/s."""
     P = ctypes.c_void_p
     G = 128
     res = {}
@@ -470,6 +471,67 @@ def bench_configs(torch, lib, ops):
                                   "frac_hbm": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)}
         del ws
     res["cfg5_lm_head_argmax"] = head
+
+    # one GPU's share when the path is split over P GPUs (N-split GEMV and
+    # lm_head, gate_up along N + down along K for the MLP); the exchanges
+    # between GPUs are not built, so these are the per-GPU kernels alone
+    shard = {}
+    for Pn in (2, 4, 8):
+        K, N = 2048, 6144 // Pn
+        nb = lin_bytes(1, K, N)
+        R = copies_for(nb)
+        ws = rand_weights(torch, N, K, G, R)
+        a = acts(1, K)
+        y = torch.empty((1, N), dtype=torch.float32, device="cuda")
+        launches = [Launcher(lib, "wq_gemv", [P(q.data_ptr()), P(sc.data_ptr()), N, K, G, P(a.xq.data_ptr()),
+                                              P(a.dx.data_ptr()), P(a.xs.data_ptr()), 1, K, 0, P(y.data_ptr())])
+                    for q, sc in ws]
+        graph_time(torch, launches, 2)
+        t = graph_time(torch, launches, max(2, 256 // R))
+        shard[f"cfg1_P{Pn}_N{N}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1)}
+        del ws
+    Vs = 151936 // 8
+    nbw = Vs * 2048 // 2 + 4 * Vs * 2048 // G
+    R = copies_for(nbw, budget=512 << 20, cap=64)
+    ws = rand_weights(torch, Vs, 2048, G, R)
+    ids = torch.arange(3 * Vs, 4 * Vs, dtype=torch.int32, device="cuda")  # shard 3's global rows
+    for M in (1, 8):
+        a = acts(M, 2048)
+        tok = torch.empty(M, dtype=torch.int32, device="cuda")
+        launches = [Launcher(lib, "wq_lm_head_argmax", [P(q.data_ptr()), P(sc.data_ptr()), Vs, 2048, G,
+                                                        P(a.xq.data_ptr()), P(a.dx.data_ptr()), P(a.xs.data_ptr()),
+                                                        M, 2048, P(ids.data_ptr()), None, P(tok.data_ptr()),
+                                                        P(wsp.data_ptr()), wsp.numel()]) for q, sc in ws]
+        graph_time(torch, launches, 2)
+        t = graph_time(torch, launches, max(2, 128 // R))
+        nb = nbw + M * 2048 + 4 * M + 4 * M * 2048 // G + 4 * M
+        shard[f"cfg5_P8_M{M}_V{Vs}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1)}
+    del ws
+    Fs = F // 8
+    nb_gu, nb_dn = lin_bytes(1, K1, 2 * Fs) - 4 * Fs, lin_bytes(1, Fs, K1)
+    R = copies_for(nb_gu + nb_dn)
+    gu = rand_weights(torch, 2 * Fs, K1, G, R)
+    dn = rand_weights(torch, K1, Fs, G, R)
+    a1 = ops.empty_acts(1, K1, None, G)
+    a2 = ops.empty_acts(1, Fs, None, G)
+    hs = torch.empty((1, Fs), dtype=torch.float32, device="cuda")
+    fused = []
+    for (qg, sg), (qd, sd) in zip(gu, dn):
+        fused.append(Launcher(lib, "wq_quant_gemv", [P(x.data_ptr()), P(nw.data_ptr()), ctypes.c_float(1e-6),
+                                                     P(qg.data_ptr()), P(sg.data_ptr()), Fs, K1, G, 1, 2,
+                                                     P(a1.xq.data_ptr()), P(a1.dx.data_ptr()), P(a1.xs.data_ptr()),
+                                                     P(hs.data_ptr())]))
+        fused.append(Launcher(lib, "wq_quant_gemv", [P(hs.data_ptr()), None, ctypes.c_float(0.0),
+                                                     P(qd.data_ptr()), P(sd.data_ptr()), K1, Fs, G, 1, 1,
+                                                     P(a2.xq.data_ptr()), P(a2.dx.data_ptr()), P(a2.xs.data_ptr()),
+                                                     P(yres.data_ptr())]))
+    graph_time(torch, fused, 2)
+    t = graph_time(torch, fused, max(2, 128 // R)) * 2
+    nb = nb_gu + 4 * Fs + Fs + 4 + 4 * (Fs // G) + nb_dn
+    shard[f"cfg2_P8_gate_up_N{2 * Fs}_down_K{Fs}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1),
+                                                     "launches": 2}
+    del gu, dn
+    res["shard_shapes"] = shard
 
     # the other producers of int8 activations: the MTP input stage
     # (mtp_in.wgsl, K = 2048) and the flash-decoding merge (attn_combine.wgsl,
