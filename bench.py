@@ -314,9 +314,11 @@ def bench_gemm(torch, lib, ops, orc, ref, args):
     """M=1024 prefill GEMMs; TOPS = 2*M*N*K / time."""
     res = {}
     P = ctypes.c_void_p
-    M = 1024
-    for K, N in ((2048, 6144), (6144, 2048)):
-        rng = np.random.default_rng(args.seed + K)
+    # M = 1024 is BASELINE's shape; 256 and 512 (the smallest prefill sizes
+    # the GEMM path serves) are reported beside it under their own keys
+    for M, K, N in ((1024, 2048, 6144), (1024, 6144, 2048), (512, 2048, 6144), (512, 6144, 2048),
+                    (256, 2048, 6144), (256, 6144, 2048)):
+        rng = np.random.default_rng(args.seed + K + (0 if M == 1024 else M))
         wq, ws = ref.make_weight(rng, N, K, 128)
         x = ref.make_activations(rng, M, K)
         copies = max(1, args.gemm_copies)  # 16: 16 x (6.3 MB weights + 25.2 MB outputs) = 504 MB
@@ -343,7 +345,7 @@ def bench_gemm(torch, lib, ops, orc, ref, args):
         graph_time(torch, launches, max(1, args.gemm_warmup))
         t = float(np.median([graph_time(torch, launches, 25) for _ in range(3)]))
         ops_ = 2.0 * M * N * K
-        res[f"K{K}_N{N}"] = {
+        res[f"K{K}_N{N}" + ("" if M == 1024 else f"_M{M}")] = {
             "us_per_launch": round(t * 1e6, 2),
             "TOPS": round(ops_ / t / 1e12, 1),
             "roofline": {"bound": "mfma", "achieved": round(ops_ / t / 1e12, 1), "peak": INT8_PEAK_TOPS,

@@ -337,6 +337,24 @@ def test_gemm_wide_tiles(K, N, G, GA, mode):
     assert np.all(np.isfinite(got))
 
 
+@pytest.mark.parametrize("M", [256, 512, 2048])
+@pytest.mark.parametrize("K,N", [(2048, 6144), (6144, 2048)])
+def test_gemm_prefill_sizes(M, K, N):
+    """The other prefill sizes, whose tile widths and grids differ from
+    M = 1024's (width 128 at M = 512 and 192 at M = 2048 for N = 6144, 64
+    elsewhere; two rounds of workgroups at M = 2048): every row of the first
+    and the last tile and one row of every 8-row group, against the oracle."""
+    note(f"gemm prefill M={M} K={K} N={N}")
+    wq, ws, x, xq, dx, xs = setup_linear(K + N + M, M, K, N, 128, None)
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, 128)
+    got = host(ops.gemm(w, dev_acts(xq, dx, xs, K, 128)))
+    idx = np.unique(np.concatenate([np.arange(0, 128), np.arange(M - 128, M),
+                                    np.arange(0, M, 8) + (np.arange(0, M, 8) // 128) % 8]))
+    want = oracle_linear_tokens(wq, ws, K, 128, xq[idx], dx[idx], xs[idx])
+    assert rel_err(got[idx], want) < 1e-5
+    assert np.all(np.isfinite(got))
+
+
 @pytest.mark.parametrize("K,N", [(2048, 6144), (6144, 2048)])
 def test_gemm_prefill_production_int32(K, N):
     """BASELINE configs[3] on the production kernel (the tile width the

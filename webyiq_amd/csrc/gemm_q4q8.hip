@@ -816,16 +816,32 @@ hipError_t launch_tile(const LinearArgs& a, hipStream_t s) {
     }
 }
 
-// Widest weight tile that still gives every CU a tile (MI355X: 256 CUs), the
-// narrowest when even that leaves CUs idle.  Mode 2 needs gate/up subtile
-// pairs per wave: widths 256 or 128.
+// Tile width: the fewest (rounds of 256 workgroups, one per CU) x (cost of
+// one tile), a tile's cost modelled as c0 + BN with c0 = 63 columns' worth of
+// fixed work (prologue, epilogue).  The model is a fit of two measured
+// launches at K = 2048, N = 6144: 256 workgroups of BN = 192 in 21.4 us and
+// 192 of BN = 64 in 10.65 us.  Against the earlier rule (the widest width
+// that still fills every CU, else the narrowest) it picks 128 at M = 512
+// (19.3 -> 15.1 us) and 192 at M = 2048 (52.0 -> 43.1 us) and the same
+// width elsewhere.  Mode 2 needs gate/up subtile pairs per wave: widths 256
+// or 128.
 int pick_bn(const LinearArgs& a) {
+    constexpr int64_t kCu = 256, kC0 = 63;
     const int64_t tm = (a.M + kBM - 1) / kBM;
-    if (a.mode == 2) return tm * ((a.N + 127) / 128) >= 256 ? 256 : 128;
-    static const int choices[] = {256, 192, 128, 64};
-    for (int bn : choices)
-        if (tm * ((a.N + bn - 1) / bn) >= 256) return bn;
-    return 64;
+    static const int widths[] = {256, 192, 128, 64};
+    int best = 64;
+    int64_t best_cost = -1;
+    for (int bn : widths) {
+        if (a.mode == 2 && bn != 256 && bn != 128) continue;
+        const int64_t outw = a.mode == 2 ? bn / 2 : bn;
+        const int64_t tiles = tm * ((a.N + outw - 1) / outw);
+        const int64_t cost = ((tiles + kCu - 1) / kCu) * (kC0 + bn);
+        if (best_cost < 0 || cost < best_cost) {
+            best = bn;
+            best_cost = cost;
+        }
+    }
+    return best;
 }
 
 template <bool DUMP>
