@@ -119,12 +119,11 @@ int wq_quant_gemv(void* stream, const float* x, const float* norm_w, float eps,
  * Prefill GEMM, any M >= 1 (tiles of 128 tokens).  Replaces Builder::gemm
  * (graph.rs:200-205) and gemm_q4q8.wgsl:46-121.  Same arguments and
  * constraints as wq_gemv, plus M * K and rows * K / 2 (rows = N, or 2N in
- * WQ_MODE_SILU_MUL) below 4 GiB.  The int32 group sums are the GEMV's; the
- * fp32 outputs of the per-token group-32 format are bit-identical to
- * wq_gemv's (same fold order); per-32 activations fold one chain per output
- * (the GEMV: chains and a tree) and the per-token group-128 format sums its
- * min term on an f16 MFMA (exact products, fp32 sums in hardware order):
- * both agree with wq_gemv within rel 1e-5.
+ * WQ_MODE_SILU_MUL) below 4 GiB.  The int32 group sums are the GEMV's; with
+ * per-token activations (G = 128 or 32) the min term is summed on an f16
+ * MFMA (exact products, fp32 sums in hardware order) and per-32 activations
+ * fold one chain per output (the GEMV: chains and a tree): the fp32 outputs
+ * agree with wq_gemv within rel 1e-5.
  */
 int wq_gemm(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K,
             int32_t G, const int8_t* xq, const float* dx, const int32_t* xs,

@@ -64,6 +64,15 @@ __device__ __forceinline__ int swz_b(int r) { return (r >> 1) & 3; }
 // banks.
 __device__ __forceinline__ int swz_p(int r) { return (r >> 1) & 7; }
 
+// f(std::integral_constant<int, I>) for I = B .. E-1, in order
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
 // 16 codes (8 packed bytes) -> 16 int8 in code order: the low nibbles of a
 // word are codes 8i..8i+3, the high nibbles 8i+4..8i+7.
 __device__ __forceinline__ v4i expand8(uint32_t w0, uint32_t w1) {
@@ -121,13 +130,14 @@ __device__ __forceinline__ void dma4_at(const void* base, uint32_t off, uint32_t
 // 4 waves on alternate K steps (two waves per SIMD, so that one wave's fold
 // overlaps the other's MFMAs), the other formats one group (their fp32 fold
 // order is fixed).
-constexpr int gemm_threads(int G, bool PT) { return PT && G == 128 ? 2 * kWaveGroup : kWaveGroup; }
+constexpr int gemm_threads(int G, bool PT) { return PT && (G == 128 || G == 32) ? 2 * kWaveGroup : kWaveGroup; }
 
 template <int BN, int G, bool PT, int MODE, bool DUMP>
 __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p) {
     constexpr int BM = kBM;
     constexpr int GE = PT ? G : 32;          // accumulation group
-    constexpr bool FAST = PT && G == 128;    // min term on the f16 MFMA
+    constexpr bool FAST = PT && (G == 128 || G == 32);  // min term on the f16 MFMA
+    constexpr bool G32 = FAST && G == 32;    // one MFMA and one fold per group
     constexpr int KS = FAST ? 2 : 1;         // wave groups splitting the K steps
     constexpr int NES = kBK / GE;            // accumulation groups per step
     constexpr int NGS = kBK / G;             // weight groups per step
@@ -281,7 +291,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     // steps) the preload's start-up cost outweighs it, 22.31 -> 22.65 us.
     const int NGPs = NG + 1 - (NG & 1);  // odd row stride
     // (the last 64-word instruction may run up to 63 words past BN rows)
-    const bool spre = FAST && nsteps >= 32 && BN * NGPs + 64 <= BN * SP_NGP;  // uniform
+    const bool spre = FAST && !G32 && nsteps >= 32 && BN * NGPs + 64 <= BN * SP_NGP;  // uniform
     const uint32_t* sp_lds = reinterpret_cast<const uint32_t*>(lds + SP_BASE);
     // Every load is unconditional (steps past the end re-read the last one),
     // so each call issues the same vector-memory instructions per wave.
@@ -513,7 +523,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
         }
     };
 
-    auto compute = [&](const int step, const int st) {
+    auto compute = [&](const int step, const int st) __attribute__((always_inline)) {
         const int8_t* Ab = As(st);
         const uint8_t* Bb = reinterpret_cast<const uint8_t*>(Bs(st));
         // 16-byte chunk c (of 4) of this step's packed weights in tile row br
@@ -530,15 +540,32 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
         if (FAST) {
             // k-slice ks of lane half h = codes 64 h + 16 ks .. +15 of the
             // group (any assignment shared by both operands gives the same
-            // sums): 32 contiguous packed bytes per lane and weight row
+            // sums): 32 contiguous packed bytes per lane and weight row.
+            // Group 32: k-slice ks = group ks, lane half h its codes
+            // 32 ks + 16 h .. +15, so that each MFMA sums one group.
             v4i af[4][TM];
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
                 const int ra = wm * 64 + 32 * i + l32;
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks)
-                    af[ks][i] = *reinterpret_cast<const v4i*>(Ab + ra * kBK + 16 * ((4 * h + ks) ^ swz_a(ra)));
+                    af[ks][i] = *reinterpret_cast<const v4i*>(
+                        Ab + ra * kBK + 16 * ((G32 ? 2 * ks + h : 4 * h + ks) ^ swz_a(ra)));
             }
+            // (group 32) the 8 packed bytes of group c, lane half h, in tile row br
+            auto bhalf = [&](int br, int c) -> uint2 {
+                return *reinterpret_cast<const uint2*>(Bb + br * 128 + 16 * ((4 * (st & 1) + c) ^ swz_p(br)) + 8 * h);
+            };
+            auto bload = [&](int br, uint4& p0, uint4& p1) {
+                if constexpr (G32) {
+                    const uint2 q0 = bhalf(br, 0), q1 = bhalf(br, 1), q2 = bhalf(br, 2), q3 = bhalf(br, 3);
+                    p0 = uint4{q0.x, q0.y, q1.x, q1.y};
+                    p1 = uint4{q2.x, q2.y, q3.x, q3.y};
+                } else {
+                    p0 = bfrag(br, 2 * h);
+                    p1 = bfrag(br, 2 * h + 1);
+                }
+            };
             // with up to 3 columns per wave, every column's packed weight
             // fragment and scale are read up front (one LDS latency per step
             // instead of one per column); wider tiles have no registers to spare
@@ -549,39 +576,64 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
                     const int br = bcol(j);
-                    pb[j][0] = bfrag(br, 2 * h);
-                    pb[j][1] = bfrag(br, 2 * h + 1);
-                    sv[j] = f16lo(Sx[br * sst]);
+                    bload(br, pb[j][0], pb[j][1]);
+                    if constexpr (!G32) sv[j] = f16lo(Sx[br * sst]);
                 }
             }
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
+            // the columns with compile-time indices (a run-time column index
+            // into facc or pb would put those arrays in scratch memory)
+            static_for<0, TN>([&](auto jc) __attribute__((always_inline)) {
+                constexpr int j = decltype(jc)::value;
                 const int br = bcol(j);
                 uint4 p0, p1;
                 if constexpr (PRE) {
                     p0 = pb[j][0];
                     p1 = pb[j][1];
                 } else {
-                    p0 = bfrag(br, 2 * h);
-                    p1 = bfrag(br, 2 * h + 1);
+                    bload(br, p0, p1);
                 }
                 const v4i bf[4] = {expand8(p0.x, p0.y), expand8(p0.z, p0.w), expand8(p1.x, p1.y),
                                    expand8(p1.z, p1.w)};
                 v16i acc[TM];
+                if constexpr (G32) {
+                    // the row's four scale words of this step (16 bytes), then
+                    // per group its two MFMAs and its fold (groups as
+                    // compile-time indices: no array is indexed at run time)
+                    const uint4 sw4 = *reinterpret_cast<const uint4*>(Sb + br * NGS);
+                    auto group = [&](auto gc, uint32_t swg, uint32_t w0, uint32_t w1) __attribute__((always_inline)) {
+                        constexpr int g = decltype(gc)::value;
+                        const v4i b = expand8(w0, w1);
 #pragma unroll
-                for (int ks = 0; ks < 4; ++ks)
+                        for (int i = 0; i < TM; ++i)
+                            acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[g][i], b, v16i{}, 0, 0, 0);
+                        const float s = f16lo(swg);
 #pragma unroll
-                    for (int i = 0; i < TM; ++i)
-                        acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks], ks == 0 ? v16i{} : acc[i],
-                                                                       0, 0, 0);
-                const float s = PRE ? sv[PRE ? j : 0] : f16lo(Sx[br * sst]);
+                        for (int i = 0; i < TM; ++i) {
+                            if (DUMP) dump(step, g, i, br, acc[i]);
 #pragma unroll
-                for (int i = 0; i < TM; ++i) {
-                    if (DUMP) dump(step, 0, i, br, acc[i]);
+                            for (int r = 0; r < 16; ++r) facc[i][j][r] = fmaf(s, (float)acc[i][r], facc[i][j][r]);
+                        }
+                    };
+                    group(std::integral_constant<int, 0>{}, sw4.x, p0.x, p0.y);
+                    group(std::integral_constant<int, 1>{}, sw4.y, p0.z, p0.w);
+                    group(std::integral_constant<int, 2>{}, sw4.z, p1.x, p1.y);
+                    group(std::integral_constant<int, 3>{}, sw4.w, p1.z, p1.w);
+                } else {
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) facc[i][j][r] = fmaf(s, (float)acc[i][r], facc[i][j][r]);
+                    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                        for (int i = 0; i < TM; ++i)
+                            acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks],
+                                                                           ks == 0 ? v16i{} : acc[i], 0, 0, 0);
+                    const float s = PRE ? sv[PRE ? j : 0] : f16lo(Sx[br * sst]);
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+                        if (DUMP) dump(step, 0, i, br, acc[i]);
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) facc[i][j][r] = fmaf(s, (float)acc[i][r], facc[i][j][r]);
+                    }
                 }
-            }
+            });
         } else {
             // one MFMA per accumulation group of 32 codes, groups in order;
             // lane half h takes codes 32 ks + 16 h .. +15
@@ -651,7 +703,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
         // instruction's offset field), not a per-step addition.
         static_assert(KS == 2 && NST == 4, "two groups on a ring of four stages");
         if constexpr (TN <= 3) {
-            auto round = [&](auto parity, int r) {
+            auto round = [&](auto parity, int r) __attribute__((always_inline)) {
                 constexpr int P = decltype(parity)::value;
                 const int sl = 2 * r + 2 + wk, sc = 2 * r + wk;
                 dma(sl, wk + 2 * (1 - P));
@@ -806,13 +858,14 @@ hipError_t launch_tile(const LinearArgs& a, hipStream_t s) {
     gp.NE = (int)(a.K / ge);
     gp.NG = (int)(a.K / a.G);
     if (a.G == 128 && pt) return launch_mode<BN, 128, true, DUMP>(gp, s);
+    if (a.G == 32 && pt) return launch_mode<BN, 32, true, DUMP>(gp, s);
     // the group-sum dump of the other formats runs widths up to 128 only
     // (launch_gemm); wider dump instances are not built
     if constexpr (DUMP && BN > 128) {
         return hipErrorInvalidConfiguration;
     } else {
         if (a.G == 128) return launch_mode<BN, 128, false, DUMP>(gp, s);
-        return pt ? launch_mode<BN, 32, true, DUMP>(gp, s) : launch_mode<BN, 32, false, DUMP>(gp, s);
+        return launch_mode<BN, 32, false, DUMP>(gp, s);
     }
 }
 
@@ -863,7 +916,7 @@ hipError_t launch_bn(const LinearArgs& a, hipStream_t s) {
 // wide dump instances exceed the register file.
 hipError_t launch_gemm(const LinearArgs& a, hipStream_t s) {
     if (!a.acc_dump) return launch_bn<false>(a, s);
-    if (a.GA == a.K && a.G == 128) return launch_bn<true>(a, s);
+    if (a.GA == a.K) return launch_bn<true>(a, s);
     return a.mode == 2 ? launch_tile<128, true>(a, s) : launch_tile<64, true>(a, s);
 }
 
