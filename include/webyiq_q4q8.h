@@ -92,8 +92,8 @@ int wq_quant_act(void* stream, const float* x, const float* norm_w, float eps,
  * per-token activations at G = 128 fold each 2048-code pass as fma chains
  * over pairs of groups and a pairwise tree over the pairs, per-32
  * activations as chains over four groups and a tree over the 16 chains, the
- * passes in order; per-token activations at G = 32 one fma chain per
- * (token, row) over the groups in index order.
+ * passes in order; per-token activations at G = 32 the same chains and tree
+ * with the token's dx applied to the total.
  */
 int wq_gemv(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K,
             int32_t G, const int8_t* xq, const float* dx, const int32_t* xs,

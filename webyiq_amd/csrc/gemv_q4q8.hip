@@ -27,8 +27,8 @@
 // row is one pass), for more through LDS, four lanes per (token, row).
 // Per-32 activation scales: per pass of 64 groups of 32, sixteen chains over
 // four consecutive groups and the pairwise tree over them, four lanes per
-// (token, row).  Per-token group 32: one fma chain per (token, row) over the
-// groups in order.
+// (token, row).  Per-token group 32: the same chains and tree with the
+// token's scale applied to the total.
 #include "argmax_combine.hpp"
 #include "common.hpp"
 #include "launch.hpp"
@@ -332,82 +332,6 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         }
     }
 
-    // fp32 epilogue of the per-token group-32 format (per-token group 128 and
-    // per-32 activations return below before using it): one chain per
-    // (token, row) over the groups in order
-    auto chain = [&](int t, int h, int rl) -> float {
-        const int32_t* ar = acc_lds + ((t * NH + h) * RB + rl) * NEP;
-        const float2* sr = sm_lds + (h * RB + rl) * NGS;
-        const float* xsr = xs_lds + t * NE;
-        const float* dr = dx_lds + t * NDX;
-        float acc = 0.0f;
-        if (PT) {
-            int ee = 0;
-            // the (A, X, s, m) operands of a block are read before its fma
-            // chain: one LDS round trip per 16 groups (same fma order)
-            auto block4 = [&](int e0, float& acc_) {
-                const int4 a4 = *reinterpret_cast<const int4*>(ar + e0);
-                const float4 x4 = *reinterpret_cast<const float4*>(xsr + e0);
-                const float4 w01 = *reinterpret_cast<const float4*>(sr + e0);
-                const float4 w23 = *reinterpret_cast<const float4*>(sr + e0 + 2);
-                acc_ = fmaf(w01.x, (float)a4.x, acc_);
-                acc_ = fmaf(w01.y, x4.x, acc_);
-                acc_ = fmaf(w01.z, (float)a4.y, acc_);
-                acc_ = fmaf(w01.w, x4.y, acc_);
-                acc_ = fmaf(w23.x, (float)a4.z, acc_);
-                acc_ = fmaf(w23.y, x4.z, acc_);
-                acc_ = fmaf(w23.z, (float)a4.w, acc_);
-                acc_ = fmaf(w23.w, x4.w, acc_);
-            };
-            if ((NE & 3) == 0) {
-                for (; ee + 16 <= NE; ee += 16) {
-                    int4 a4[4];
-                    float4 x4[4], w01[4], w23[4];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        a4[q] = *reinterpret_cast<const int4*>(ar + ee + 4 * q);
-                        x4[q] = *reinterpret_cast<const float4*>(xsr + ee + 4 * q);
-                        w01[q] = *reinterpret_cast<const float4*>(sr + ee + 4 * q);
-                        w23[q] = *reinterpret_cast<const float4*>(sr + ee + 4 * q + 2);
-                    }
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        acc = fmaf(w01[q].x, (float)a4[q].x, acc);
-                        acc = fmaf(w01[q].y, x4[q].x, acc);
-                        acc = fmaf(w01[q].z, (float)a4[q].y, acc);
-                        acc = fmaf(w01[q].w, x4[q].y, acc);
-                        acc = fmaf(w23[q].x, (float)a4[q].z, acc);
-                        acc = fmaf(w23[q].y, x4[q].z, acc);
-                        acc = fmaf(w23[q].z, (float)a4[q].w, acc);
-                        acc = fmaf(w23[q].w, x4[q].w, acc);
-                    }
-                }
-                for (; ee < NE; ee += 4) block4(ee, acc);
-            }
-#pragma unroll 8
-            for (; ee < NE; ++ee) {
-                float2 w = sr[ee];
-                acc = fmaf(w.x, (float)ar[ee], acc);
-                acc = fmaf(w.y, xsr[ee], acc);
-            }
-            return acc * dr[0];
-        } else {
-            (void)dr;
-            return acc;  // not reached: per-32 activations take the four-lane epilogue
-        }
-    };
-    // y of (token t, local row rl) from its chain(s)
-    auto finish = [&](int t, int rl) {
-        const float v = chain(t, 0, rl);
-        float* yo = a.y + (int64_t)t * N + r0 + rl;
-        if (MODE == 0) {
-            *yo = v;
-        } else if (MODE == 1) {
-            *yo = *yo + v;
-        } else {
-            *yo = silu_mul(v, chain(t, 1, rl));
-        }
-    };
     if constexpr (PT && G == 128 && MT == 1) {
         // Per-token group-128 epilogue in registers (one token: few outputs
         // per workgroup, so latency matters more than lane occupancy).
@@ -655,13 +579,15 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         return;
     }
 
-    if constexpr (!PT) {
+    if constexpr (!PT || G == 32) {
         // Per-32 activation scales: four lanes per (token, row).  Per pass of
         // 64 groups of 32, lane q runs the chains c = fma(s dx, A, c);
         // c = fma(m dx, X, c) from 0 over groups 16q + 4i .. 16q + 4i + 3
         // (i = 0..3) and forms (c0 + c1) + (c2 + c3); two quad moves complete
         // the pairwise tree over the pass's 16 chains; the pass sums are
-        // added in order.  The oracle's order.
+        // added in order.  Per-token group 32: the same with the token's dx
+        // outside, c = fma(s, A, c); c = fma(m, X, c) and total * dx.  The
+        // oracle's order.
         unsigned long long* keys = lds_align<8, unsigned long long>(smem, dx_lds + (size_t)MT * NDX);
         for (int o = tid; o < 4 * MT * RB; o += nthreads) {
             const int q = o & 3, oo = o >> 2;
@@ -683,7 +609,9 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
                         if (eb < NE) {
                             const int4 a4 = *reinterpret_cast<const int4*>(ar + eb);
                             const float4 x4 = *reinterpret_cast<const float4*>(xsr + eb);
-                            const float4 d4 = *reinterpret_cast<const float4*>(dr + eb);
+                            // (per token: dx is applied to the total)
+                            const float4 d4 = PT ? make_float4(1.f, 1.f, 1.f, 1.f)
+                                                 : *reinterpret_cast<const float4*>(dr + eb);
                             float2 w0, w1, w2, w3;
                             if constexpr (G == 128) {  // the four groups share one weight group
                                 w0 = w1 = w2 = w3 = sr[eb / 4];
@@ -695,14 +623,25 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
                                 w2 = make_float2(w23.x, w23.y);
                                 w3 = make_float2(w23.z, w23.w);
                             }
-                            v = fmaf(w0.x * d4.x, (float)a4.x, v);
-                            v = fmaf(w0.y * d4.x, x4.x, v);
-                            v = fmaf(w1.x * d4.y, (float)a4.y, v);
-                            v = fmaf(w1.y * d4.y, x4.y, v);
-                            v = fmaf(w2.x * d4.z, (float)a4.z, v);
-                            v = fmaf(w2.y * d4.z, x4.z, v);
-                            v = fmaf(w3.x * d4.w, (float)a4.w, v);
-                            v = fmaf(w3.y * d4.w, x4.w, v);
+                            if constexpr (PT) {
+                                v = fmaf(w0.x, (float)a4.x, v);
+                                v = fmaf(w0.y, x4.x, v);
+                                v = fmaf(w1.x, (float)a4.y, v);
+                                v = fmaf(w1.y, x4.y, v);
+                                v = fmaf(w2.x, (float)a4.z, v);
+                                v = fmaf(w2.y, x4.z, v);
+                                v = fmaf(w3.x, (float)a4.w, v);
+                                v = fmaf(w3.y, x4.w, v);
+                            } else {
+                                v = fmaf(w0.x * d4.x, (float)a4.x, v);
+                                v = fmaf(w0.y * d4.x, x4.x, v);
+                                v = fmaf(w1.x * d4.y, (float)a4.y, v);
+                                v = fmaf(w1.y * d4.y, x4.y, v);
+                                v = fmaf(w2.x * d4.z, (float)a4.z, v);
+                                v = fmaf(w2.y * d4.z, x4.z, v);
+                                v = fmaf(w3.x * d4.w, (float)a4.w, v);
+                                v = fmaf(w3.y * d4.w, x4.w, v);
+                            }
                         }
                         c[i] = v;
                     }
@@ -711,7 +650,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
                     v = v + dpp_f<kDppXor2>(v);
                     total = e0 == 0 ? v : total + v;
                 }
-                tot[h] = total;
+                tot[h] = PT ? total * dr[0] : total;
             }
             if (q != 0) continue;
             const int64_t row = r0 + rl;
@@ -743,31 +682,6 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         }
         return;
     }
-
-    if (!ARGMAX) {
-        for (int o = tid; o < MT * RB; o += nthreads) {
-            const int t = MT == 1 ? 0 : o / RB, rl = o - t * RB;
-            if (t < a.M && r0 + rl < N) finish(t, rl);
-        }
-        return;
-    }
-
-    // fused greedy argmax (argmax.wgsl:19-34 tie rule), one key per (t, row)
-    unsigned long long* keys = lds_align<8, unsigned long long>(smem, dx_lds + (size_t)MT * NDX);
-    for (int o = tid; o < MT * RB; o += nthreads) {
-        const int t = o / RB, rl = o - t * RB;
-        const int64_t row = r0 + rl;
-        unsigned long long key = 0;
-        if (t < a.M && row < N) {
-            float v = chain(t, 0, rl);
-            if (a.y) a.y[(int64_t)t * N + row] = v;
-            if (v > -3.0e38f) key = argmax_key(v, (uint32_t)row);
-        }
-        keys[o] = key;
-    }
-    __syncthreads();
-    const unsigned long long best = block_best<MT>(keys, RB, (int)a.M);
-    argmax_combine<MT>(p.am, (int)a.M, p.nblocks, best);
 }
 
 // ------------------------------------------------------------ dispatch ----
