@@ -199,7 +199,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
         }
     }
 
-    // 4. fp32 epilogue: one chain per (token, row) over the groups in order
+    // 4. fp32 epilogue per (token, row), in the dot4 kernel's group-128 order
     auto chain = [&](int t, int h, int rl) -> float {
         const int32_t* ar = acc_lds + ((t * NH + h) * RB + rl) * NGP;
         const float2* sr = sm_lds + (h * RB + rl) * NGP;
