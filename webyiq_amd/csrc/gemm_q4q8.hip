@@ -19,12 +19,12 @@
 // so that the 16-byte fragment reads of consecutive rows hit distinct banks.
 //
 // Folding the exact group sums into fp32 is VALU work per output element per
-// group, as much issue time as the MFMAs themselves.  The per-token group-128
-// format keeps it at two instructions, acc = fma(s, float(A), acc), and
-// computes the min term sum_g m * X up front on the f16 MFMA: X = 64 * X_hi +
-// X_lo with 64 * X_hi and X_lo exact in f16 (|X| <= 128 * 127), so each
-// product with the f16 m is exact.  Other formats (group 32, per-32 activation
-// scales) fold both terms on the VALU in the GEMV's order, bit for bit.  Tiles
+// group, as much issue time as the MFMAs themselves.  The per-token formats
+// (group 128, and group 32 with one MFMA pair and one fold per group) keep it
+// at two instructions, acc = fma(s, float(A), acc), and compute the min term
+// sum_g m * X up front on the f16 MFMA: X = 64 * X_hi + X_lo with 64 * X_hi
+// and X_lo exact in f16 (|X| <= 128 * 127), so each product with the f16 m
+// is exact.  Per-32 activation scales fold both terms on the VALU.  Tiles
 // are assigned XCD by XCD so that the workgroups sharing a weight tile share
 // one L2.
 #include <type_traits>
@@ -592,8 +592,6 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
                 } else {
                     bload(br, p0, p1);
                 }
-                const v4i bf[4] = {expand8(p0.x, p0.y), expand8(p0.z, p0.w), expand8(p1.x, p1.y),
-                                   expand8(p1.z, p1.w)};
                 v16i acc[TM];
                 if constexpr (G32) {
                     // the row's four scale words of this step (16 bytes), then
@@ -619,6 +617,8 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
                     group(std::integral_constant<int, 2>{}, sw4.z, p1.x, p1.y);
                     group(std::integral_constant<int, 3>{}, sw4.w, p1.z, p1.w);
                 } else {
+                    const v4i bf[4] = {expand8(p0.x, p0.y), expand8(p0.z, p0.w), expand8(p1.x, p1.y),
+                                       expand8(p1.z, p1.w)};
 #pragma unroll
                     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
