@@ -375,7 +375,8 @@ def copies_for(nbytes, budget=512 << 20, cap=1024):
 
 def bench_configs(torch, lib, ops):
     """BASELINE configs 2, 3 and 5 (decode MLP block, M<=8 verify shapes,
-    lm_head + argmax) and one GPU's share of them when split over 2-8 GPUs:
+    lm_head + argmax), one GPU's share of them when split over 2-8 GPUs, and
+    the group-32 format on the cfg-1/2/4 shapes:
     us per launch (graph replays over weight copies, so weights stream from
     HBM) and algorithmic GB/s."""
     P = ctypes.c_void_p
@@ -534,6 +535,35 @@ def bench_configs(torch, lib, ops):
                                                      "launches": 2}
     del gu, dn
     res["shard_shapes"] = shard
+
+    # the converter's native group size (G = 32, per-token activations) on
+    # the cfg-1 / cfg-2 down GEMVs and the cfg-4 GEMM shape
+    g32 = {}
+    for M, K, N in ((1, 2048, 6144), (1, 6144, 2048), (8, 2048, 6144)):
+        nb = gemv_bytes(M, K, N, 32)
+        R = copies_for(nb)
+        ws = rand_weights(torch, N, K, 32, R)
+        a = ops.quant(torch.randn((M, K), dtype=torch.float32, device="cuda"), G=32)
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        launches = [Launcher(lib, "wq_gemv", [P(q.data_ptr()), P(sc.data_ptr()), N, K, 32, P(a.xq.data_ptr()),
+                                              P(a.dx.data_ptr()), P(a.xs.data_ptr()), M, K, 0, P(y.data_ptr())])
+                    for q, sc in ws]
+        graph_time(torch, launches, 2)
+        t = graph_time(torch, launches, max(2, 256 // R))
+        g32[f"gemv_M{M}_K{K}_N{N}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1)}
+        del ws
+    M, K, N = 1024, 2048, 6144
+    ws = rand_weights(torch, N, K, 32, 8)
+    a = ops.quant(torch.randn((M, K), dtype=torch.float32, device="cuda"), G=32)
+    ys = [torch.empty((M, N), dtype=torch.float32, device="cuda") for _ in range(8)]
+    launches = [Launcher(lib, "wq_gemm", [P(q.data_ptr()), P(sc.data_ptr()), N, K, 32, P(a.xq.data_ptr()),
+                                          P(a.dx.data_ptr()), P(a.xs.data_ptr()), M, K, 0, P(ys[i].data_ptr())])
+                for i, (q, sc) in enumerate(ws)]
+    graph_time(torch, launches, 50)
+    t = graph_time(torch, launches, 10)
+    g32[f"gemm_M{M}_K{K}_N{N}"] = {"us": round(t * 1e6, 2), "TOPS": round(2.0 * M * N * K / t / 1e12, 1)}
+    del ws, ys
+    res["group32"] = g32
 
     # the other producers of int8 activations: the MTP input stage
     # (mtp_in.wgsl, K = 2048) and the flash-decoding merge (attn_combine.wgsl,
