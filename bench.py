@@ -18,7 +18,10 @@ Printed JSON line:
               a copy-kernel calibration) when profiles/gemv_traffic.json
               holds them
   prefill     the M=1024 GEMMs (K=2048 N=6144 and K=6144 N=2048): us, TOPS
-              and fraction of the 5.0 POP/s dense int8 MFMA peak
+              and fraction of the 5.0 POP/s dense int8 MFMA peak; the same
+              shapes at M=256 and 512 under keys ending _M256 / _M512
+  configs     BASELINE configs 2, 3 and 5, the decode layer, the other
+              producers, one GPU's shard shapes, the group-32 format
   cpu_baseline the reference's torch fake-quant path (oracle/reference.py) on a
               bounded sample of the same workload on this host's cores
 Algorithmic bytes: W = N*K/2, S = 4*N*K/G, x = M*K + 4*M + 4*M*K/G, y = 4*M*N.
