@@ -4,11 +4,14 @@
   python bench.py [--steps K] [--warmup W] [--copies R] [--no-cpu] [--gpus 1]
 
 One step = one decode GEMV launch (M=1, K=2048, N=6144, int4 group-128 weights,
-per-token int8 activations) on inputs already resident in HBM.  Launches rotate
-over R weight copies (default 64 x 6.7 MB = 430 MB > the 256 MB MALL), so every
-launch streams its weights from HBM.  The timed K steps run as HIP-graph
-replays (no host gap between launches) bracketed by synchronize on both sides;
-HIP events on the replay stream time the region.
+per-token int8 activations) on inputs already resident in HBM.  W warm-up
+launches, then exactly K timed launches; launch i uses weight copy i mod R
+(default R = 64 x 6.7 MB = 430 MB > the 256 MB MALL), so every launch streams
+its weights from HBM.  The K launches are captured as one HIP graph (or, with
+--launch eager, issued directly) and queued behind a gate of passes over a
+512 MiB buffer, so the GPU runs them back to back with no host submission
+gap; HIP events on that stream around the K launches time the region, which
+is synchronised on both sides.
 
 Printed JSON line:
   value       whole-job GEMV throughput, algorithmic GB/s over the K steps
@@ -16,10 +19,13 @@ Printed JSON line:
               over the timed region, against 8 TB/s; traffic = HBM bytes per
               launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE, scaled by
               a copy-kernel calibration) when profiles/gemv_traffic.json
-              holds them
+              holds them; kernel_us = one launch's device-clock duration
+              (first workgroup entry to last store, the timing build) and
+              kernel_frac the same bytes over it
   prefill     the M=1024 GEMMs (K=2048 N=6144 and K=6144 N=2048): us, TOPS
-              and fraction of the 5.0 POP/s dense int8 MFMA peak; the same
-              shapes at M=256 and 512 under keys ending _M256 / _M512
+              and fraction of the 5.0 POP/s dense int8 MFMA peak as flat
+              keys <shape>_us/_TOPS/_frac; the same shapes at M=256 and 512
+              under keys with _M256 / _M512; prefill_detail per shape
   configs     BASELINE configs 2, 3 and 5, the decode layer, the other
               producers, one GPU's shard shapes, the group-32 format
   cpu_baseline the reference's torch fake-quant path (oracle/reference.py) on a
@@ -27,7 +33,8 @@ Printed JSON line:
 Algorithmic bytes: W = N*K/2, S = 4*N*K/G, x = M*K + 4*M + 4*M*K/G, y = 4*M*N.
 Parity gates before timing: the GEMV bit-exact against the CPU oracle; the
 GEMM (per-token group-128, min term on the f16 MFMA) within rel 1e-5 on
-sampled tokens.
+sampled tokens; every cfg-2/3/5 instance and the one-token decode layer
+(configs.parity_gates).
 """
 import argparse
 import ctypes
@@ -63,9 +70,9 @@ def parse():
                     help="weight/output copies the prefill GEMMs rotate over (16 = 504 MB, twice the MALL)")
     ap.add_argument("--gemm-warmup", type=int, default=400,
                     help="graph replays before the prefill GEMMs are timed (clocks settle within ~80 ms)")
-    ap.add_argument("--floor", action="store_true",
-                    help="also time the no-arithmetic kernels of bench_floor.hip on the GEMV's grid "
-                         "and weight copies, alternating with the GEMV (per-launch floors)")
+    ap.add_argument("--launch", choices=("graph", "eager"), default="graph",
+                    help="timed launches as one captured HIP graph (default) or as eager launches "
+                         "(both queued behind the gate kernel)")
     ap.add_argument("--timeline", action="store_true",
                     help="also replay the GEMV from the timing build (libwebyiq_q4q8_timeline.so) and "
                          "report its per-workgroup phase stamps")
@@ -116,6 +123,53 @@ def graph_time(torch, launches, reps):
     return e0.elapsed_time(e1) * 1e-3 / (reps * len(launches))
 
 
+class Gate:
+    """Host-independent timing of a launch sequence.  On the launch stream, a
+    gate of passes over a 512 MiB buffer (each pass reads and writes it all,
+    ~0.2 ms) runs first, long enough for the host to enqueue the whole
+    sequence behind it; then e0, the sequence, e1.  The event interval holds
+    the GPU's back-to-back launches and no host submission gap, whatever the
+    sequence length, and the gate leaves no weight copy of the sequence in
+    the 256 MB MALL.  Synchronised on both sides."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.flush = torch.zeros(128 << 20, dtype=torch.float32, device="cuda")
+
+    def time(self, seq, graph=True, host_us_per_launch=20.0):
+        """Seconds per launch of `seq` (callables taking a stream)."""
+        torch = self.torch
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = None
+        if graph:
+            with torch.cuda.stream(s):
+                for ln in seq[:1]:
+                    ln(ctypes.c_void_p(s.cuda_stream))
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                cs = ctypes.c_void_p(s.cuda_stream)
+                for ln in seq:
+                    ln(cs)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        passes = 2 + int(host_us_per_launch * len(seq) / 150.0)
+        with torch.cuda.stream(s):
+            for _ in range(passes):
+                self.flush.add_(1.0)
+            e0.record(s)
+            if g is not None:
+                g.replay()
+            else:
+                cs = ctypes.c_void_p(s.cuda_stream)
+                for ln in seq:
+                    ln(cs)
+            e1.record(s)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / len(seq)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -160,16 +214,19 @@ def main():
     launches = [Launcher(lib, "wq_gemv", [P(qs[i].data_ptr()), P(ss[i].data_ptr()), N, K, G,
                                           P(a.xq.data_ptr()), P(a.dx.data_ptr()), P(a.xs.data_ptr()),
                                           M, K, 0, P(y.data_ptr())]) for i in range(R)]
-    # warm-up, then the timed steps as graph replays
-    reps_w = max(1, args.warmup // R)
-    graph_time(torch, launches, reps_w)
-    reps = max(1, args.steps // R)
-    t_launch = graph_time(torch, launches, reps)
-    steps = reps * R
+    # warm-up: W launches on copies 0 .. W-1 (mod R); then exactly K timed
+    # launches on copies W, W+1, ... (mod R): a copy comes back only after R
+    # launches (430 MB), so every timed launch streams its weights from HBM
+    steps, warmup = max(1, args.steps), max(0, args.warmup)
+    gate = Gate(torch)
+    graph = args.launch == "graph"
+    if warmup:
+        gate.time([launches[i % R] for i in range(warmup)], graph=graph)
+    t_launch = gate.time([launches[(warmup + i) % R] for i in range(steps)], graph=graph)
     nbytes = gemv_bytes(M, K, N, G)
     value = nbytes / t_launch / 1e9
-    # the kernel's mean duration per launch over the timed region (graph
-    # replays back to back, HIP events on the replay stream)
+    # the kernel's mean duration per launch over the timed region (HIP events
+    # on the launch stream around the K launches)
     achieved = nbytes / t_launch / 1e9
 
     traffic = None
@@ -183,11 +240,7 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": reps_w * R,
-        # timed launches are whole rotations over the R weight copies (so every
-        # launch streams from HBM): the counts above are the requests rounded up
-        "steps_requested": args.steps,
-        "warmup_requested": args.warmup,
+        "warmup": warmup,
         "ms_per_step": round(t_launch * 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",
@@ -197,14 +250,19 @@ def main():
         "config": {"workload": "decode GEMV M=1 K=2048 N=6144 G=128 per-token int8 (BASELINE configs[0] shape)",
                    "M": M, "K": K, "N": N, "G": G, "weight_copies": R,
                    "bytes_per_launch": nbytes, "parallelism": "single GPU"},
-        "gemv_us_per_launch_graph": round(t_launch * 1e6, 3),
+        "gemv_us_per_launch": round(t_launch * 1e6, 3),
+        "launch": args.launch,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "parity": {"gemv_vs_oracle_bit_exact": parity},
     }
-
-    if args.floor:
-        out["floor"] = bench_floor(torch, launches, qs, ss, N)
+    kc = kernel_clock(torch, gate, [ln.args for ln in launches])
+    if kc is not None:
+        # the device-clock duration of one launch (first workgroup entry to
+        # last store, the timing build), beside the per-launch figure above
+        out["roofline"]["kernel_us"] = kc["median_us"]
+        out["roofline"]["kernel_frac"] = round(nbytes / (kc["median_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+        out["kernel_clock"] = kc
 
     if args.timeline:
         out["timeline"] = bench_timeline(torch, [ln.args for ln in launches])
@@ -220,10 +278,15 @@ def main():
         del src, dst
 
     if not args.no_gemm:
-        out["prefill"] = bench_gemm(torch, lib, ops, orc, ref, args)
+        detail = bench_gemm(torch, lib, ops, orc, ref, args)
+        # flat scalars per shape (us, TOP/s, fraction of the int8 peak); the
+        # per-shape roofline blocks and parity figures under prefill_detail
+        out["prefill"] = {f"{k}_{f}": v[src] for k, v in detail.items()
+                          for f, src in (("us", "us_per_launch"), ("TOPS", "TOPS"), ("frac", "frac"))}
+        out["prefill_detail"] = detail
 
     if not args.no_configs:
-        out["configs"] = bench_configs(torch, lib, ops)
+        out["configs"] = bench_configs(torch, lib, ops, orc)
 
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(torch, ref, wq, ws, K, G, x, nbytes, args.cpu_seconds)
@@ -231,48 +294,47 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-def bench_floor(torch, gemv_launches, qs, ss, N):
-    """Per-launch graph-replay time of bench_floor.hip's kernels (empty; read
-    the weight rows and scale words; read and store one word per row) on the
-    GEMV's grid and weight copies, alternating with the GEMV itself over three
-    rounds (medians, us)."""
-    F = ctypes.CDLL(os.path.join(HERE, "bench_floor.so"))
-    F.floor_launch.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
-                               ctypes.c_int]
-    F.floor_launch.restype = ctypes.c_int
-    out = torch.zeros(N, dtype=torch.int32, device="cuda")
-    P = ctypes.c_void_p
+def timeline_lib():
+    """The timing build (libwebyiq_q4q8_timeline.so: the same kernels, the
+    decode GEMV's thread 0 per workgroup stamping s_memrealtime, a 100 MHz
+    clock), or None when it has not been built."""
+    from webyiq_amd import _lib
+    path = os.path.join(HERE, "webyiq_amd", "libwebyiq_q4q8_timeline.so")
+    if not os.path.exists(path):
+        return None
+    T = ctypes.CDLL(path)
+    T.wq_gemv.argtypes, T.wq_gemv.restype = _lib.PROTOTYPES["wq_gemv"]
+    T.wq_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    T.wq_timeline_read.restype = ctypes.c_int
+    return T
 
-    class Floor:
-        def __init__(self, kind, i):
-            self.args = (kind, P(qs[i].data_ptr()), P(ss[i].data_ptr()), P(out.data_ptr()), N)
 
-        def __call__(self, stream):
-            rc = F.floor_launch(stream, *self.args)
-            if rc != 0:
-                raise RuntimeError(f"floor launch failed [{rc}]")
+def read_stamps(T):
+    buf = np.zeros(4096 * 8, dtype=np.uint64)
+    if T.wq_timeline_read(buf.ctypes.data, buf.nbytes) != 0:
+        raise RuntimeError("wq_timeline_read failed")
+    b = buf.reshape(4096, 8).astype(np.int64)
+    return b[b[:, 0] > 0]
 
-    R = len(qs)
-    sets = {"empty": [Floor(0, i) for i in range(R)], "read": [Floor(1, i) for i in range(R)],
-            "read_store": [Floor(2, i) for i in range(R)], "gemv": gemv_launches}
-    times = {k: [] for k in sets}
-    for k, lns in sets.items():
-        graph_time(torch, lns, 10)
-    for _ in range(3):
-        for k, lns in sets.items():
-            times[k].append(graph_time(torch, lns, 20) * 1e6)
-    res = {f"{k}_us": round(float(np.median(v)), 3) for k, v in times.items()}
-    res["grid"] = "768 workgroups x 4 waves, 2 rows per wave (the GEMV's plan at M=1, K=2048, N=6144)"
-    # the empty kernel on other grids (256 threads each): per-launch cost against grid size
-    res["empty_us_by_workgroups"] = {}
-    for nwg in (1, 256, 768, 1536, 3072, 4096):
-        lns = [Floor(3, 0) for _ in range(R)]
-        for ln in lns:
-            ln.args = (3, P(qs[0].data_ptr()), P(ss[0].data_ptr()), P(out.data_ptr()), nwg)
-        graph_time(torch, lns, 5)
-        res["empty_us_by_workgroups"][str(nwg)] = round(graph_time(torch, lns, 20) * 1e6, 3)
-    res["bytes_read"] = int(N * (1024 + 64))
-    return res
+
+def kernel_clock(torch, gate, launch_args, n=32):
+    """Device-clock duration of single headline launches: n launches of the
+    timing build, each on a different weight copy after the MALL flush, each
+    from the first workgroup's entry stamp to the last workgroup's
+    after-store stamp (us; median and range)."""
+    T = timeline_lib()
+    if T is None:
+        return None
+    durs = []
+    for i in range(n):
+        ln = Launcher(T, "wq_gemv", list(launch_args[i % len(launch_args)]))
+        gate.time([ln], graph=False, host_us_per_launch=50.0)
+        b = read_stamps(T)
+        durs.append((b[:, 4].max() - b[:, 0].min()) / 100.0)
+    return {"median_us": round(float(np.median(durs)), 3), "min_us": round(float(np.min(durs)), 3),
+            "max_us": round(float(np.max(durs)), 3), "launches": n,
+            "how": "timing build, s_memrealtime (100 MHz): first workgroup entry to last workgroup's "
+                   "after-store stamp, single cold launches"}
 
 
 def bench_timeline(torch, launch_args):
@@ -351,6 +413,7 @@ def bench_gemm(torch, lib, ops, orc, ref, args):
         res[f"K{K}_N{N}" + ("" if M == 1024 else f"_M{M}")] = {
             "us_per_launch": round(t * 1e6, 2),
             "TOPS": round(ops_ / t / 1e12, 1),
+            "frac": round(ops_ / t / 1e12 / INT8_PEAK_TOPS, 4),
             "roofline": {"bound": "mfma", "achieved": round(ops_ / t / 1e12, 1), "peak": INT8_PEAK_TOPS,
                          "unit": "TOP/s", "frac": round(ops_ / t / 1e12 / INT8_PEAK_TOPS, 4)},
             "parity_vs_oracle_rel": rel,
@@ -376,15 +439,50 @@ def copies_for(nbytes, budget=512 << 20, cap=1024):
     return max(2, min(cap, -(-budget // nbytes)))
 
 
-def bench_configs(torch, lib, ops):
+def to_host_u32(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+def oracle_rows(orc, wq, ws, K, G, xq, dx, xs, threads=16):
+    """orc.linear (mode 0) split along the weight rows over a thread pool
+    (ctypes releases the GIL during the C oracle's calls)."""
+    from concurrent.futures import ThreadPoolExecutor
+    N = wq.shape[0]
+    n = max(1, min(threads, os.cpu_count() or 1, N // 1024 or 1))
+    cuts = np.linspace(0, N, n + 1).astype(int)
+    with ThreadPoolExecutor(n) as ex:
+        parts = ex.map(lambda i: orc.linear(wq[cuts[i]:cuts[i + 1]], ws[cuts[i]:cuts[i + 1]], K, G, xq, dx, xs),
+                       range(n))
+        return np.concatenate(list(parts), 1)
+
+
+def parity_gate(name, ok, detail=""):
+    """Stop the bench when a timed instance's output differs from the oracle."""
+    if not ok:
+        print(f"bench.py: {name} differs from the oracle {detail}", file=sys.stderr)
+        sys.exit(1)
+    return True
+
+
+def bench_configs(torch, lib, ops, orc):
     """BASELINE configs 2, 3 and 5 (decode MLP block, M<=8 verify shapes,
     lm_head + argmax), one GPU's share of them when split over 2-8 GPUs, and
     the group-32 format on the cfg-1/2/4 shapes:
     us per launch (graph replays over weight copies, so weights stream from
-    HBM) and algorithmic GB/s."""
+    HBM) and algorithmic GB/s.  Before timing, every cfg-2/3/5 instance and
+    the one-token decode layer are checked against the oracle on the timed
+    inputs (one launch on the first weight copy): GEMV outputs bit-exact
+    (mode 2 within rel 1e-5), argmax tokens exact, the fused layer
+    bit-identical to the unfused one with its first projection bit-exact."""
     P = ctypes.c_void_p
     G = 128
     res = {}
+    gates = {}
+    cur = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+
+    def host_acts(a):
+        torch.cuda.synchronize()
+        return a.xq.cpu().numpy(), a.dx.cpu().numpy(), a.xs.cpu().numpy()
 
     def acts(M, K):
         x = torch.randn((M, K), dtype=torch.float32, device="cuda")
@@ -407,6 +505,10 @@ def bench_configs(torch, lib, ops):
             launches = [Launcher(lib, "wq_gemv", [P(q.data_ptr()), P(sc.data_ptr()), N, K, G,
                                                   P(a.xq.data_ptr()), P(a.dx.data_ptr()), P(a.xs.data_ptr()),
                                                   M, K, 0, P(y.data_ptr())]) for q, sc in ws]
+            launches[0](cur())
+            want = orc.linear(to_host_u32(ws[0][0]), to_host_u32(ws[0][1]), K, G, *host_acts(a))
+            gates[f"cfg3_M{M}_{name}"] = parity_gate(
+                f"cfg 3 M={M} {name}", np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32)))
             graph_time(torch, launches, 2)
             t = graph_time(torch, launches, max(2, 256 // R))
             verify[f"M{M}_{name}_K{K}_N{N}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1)}
@@ -436,6 +538,21 @@ def bench_configs(torch, lib, ops):
                                                      P(qd.data_ptr()), P(sd.data_ptr()), K1, F, G, 1, 1,
                                                      P(a2.xq.data_ptr()), P(a2.dx.data_ptr()), P(a2.xs.data_ptr()),
                                                      P(yres.data_ptr())]))
+    # gate: one block from a zero residual against the oracle chain
+    yres.zero_()
+    fused[0](cur())
+    fused[1](cur())
+    xh = x.cpu().numpy()
+    q1, d1, s1 = orc.quant_act(xh, None, G, norm_w=nw.cpu().numpy(), eps=1e-6)
+    h_want = orc.linear(to_host_u32(gu[0][0]), to_host_u32(gu[0][1]), K1, G, q1, d1, s1, mode=2)
+    h_got = h.cpu().numpy()
+    rel_h = float(np.max(np.abs(h_got - h_want)) / max(float(np.max(np.abs(h_want))), 1e-30))
+    q2, d2, s2 = orc.quant_act(h_got, None, G)
+    y_want = orc.linear(to_host_u32(dn[0][0]), to_host_u32(dn[0][1]), F, G, q2, d2, s2, mode=1,
+                        y=np.zeros((1, K1), np.float32))
+    gates["cfg2_block"] = parity_gate(
+        "cfg 2 block", rel_h < 1e-5 and np.array_equal(host_acts(a2)[0], q2)
+        and np.array_equal(yres.cpu().numpy().view(np.uint32), y_want.view(np.uint32)), f"(gate_up rel {rel_h:.3g})")
     graph_time(torch, fused, 2)
     t2 = graph_time(torch, fused, max(2, 128 // R)) * 2  # per block (2 launches)
     steps = []
@@ -470,6 +587,10 @@ def bench_configs(torch, lib, ops):
                                                             P(a.xq.data_ptr()), P(a.dx.data_ptr()), P(a.xs.data_ptr()),
                                                             M, 2048, None, None, P(tok.data_ptr()),
                                                             P(wsp.data_ptr()), wsp.numel()]) for q, sc in ws]
+            launches[0](cur())
+            logits = oracle_rows(orc, to_host_u32(ws[0][0]), to_host_u32(ws[0][1]), 2048, G, *host_acts(a))
+            gates[f"cfg5_M{M}_V{V}"] = parity_gate(
+                f"cfg 5 M={M} V={V}", np.array_equal(tok.cpu().numpy().view(np.uint32), orc.argmax(logits)))
             graph_time(torch, launches, 2)
             t = graph_time(torch, launches, max(2, 64 // R))
             nb = nbw + M * 2048 + 4 * M + 4 * M * 2048 // G + 4 * M
@@ -625,6 +746,28 @@ def bench_configs(torch, lib, ops):
             layers.append(DecodeLayer(w, M, hidden=H, q_dim=Q, kv_dim=KV, ffn=F, G=G, fused=fuse, x=x,
                                       attention=attention))
         x0 = torch.randn((M, H), dtype=torch.float32, device="cuda")
+        if M == 1 and fuse and attention == "combine":
+            # gate: the first layer, fused, against the unfused sequence on the
+            # same weights and partials (bit-identical) and its qkv against the
+            # oracle (bit-exact)
+            lay0 = layers[0]
+            twin = DecodeLayer(lay0.w, M, hidden=H, q_dim=Q, kv_dim=KV, ffn=F, G=G, fused=False,
+                               attention=attention)
+            twin.part.copy_(lay0.part)
+            x.copy_(x0)
+            lay0.run()
+            twin.x.copy_(x0)
+            twin.run()
+            torch.cuda.synchronize()
+            wq0 = lay0.w.w("qkv")
+            qq, qd, qs_ = orc.quant_act(x0.cpu().numpy(), None, G, norm_w=lay0.w["attn_norm"].cpu().numpy(),
+                                        eps=1e-6)
+            qkv_want = orc.linear(to_host_u32(wq0.q), to_host_u32(wq0.s), H, G, qq, qd, qs_)
+            gates["decode_layer_M1"] = parity_gate(
+                "decode layer M=1", np.array_equal(x.cpu().numpy().view(np.uint32),
+                                                   twin.x.cpu().numpy().view(np.uint32))
+                and np.array_equal(lay0.qkv.cpu().numpy().view(np.uint32), qkv_want.view(np.uint32)))
+            del twin
 
         class Step:  # the graph_time launch protocol: one callable per captured unit
             def __call__(self, stream):
@@ -643,19 +786,30 @@ def bench_configs(torch, lib, ops):
                      "attention_stand_in": attention, "weight_GBps": round(nbw / t / 1e9, 1)}
         del layers
     res["decode_step_graph"] = step
+    res["parity_gates"] = {"checked": len(gates), "all_passed": all(gates.values())}
     torch.cuda.empty_cache()
     return res
 
 
 def cpu_model():
+    """The host CPU as /proc/cpuinfo names it: model name, plus the family
+    and model numbers (a virtualised host may give only a generic name)."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                k, _, v = line.partition(":")
+                k = k.strip()
+                if k in ("model name", "cpu family", "model", "vendor_id") and k not in info:
+                    info[k] = v.strip()
+                if not line.strip() and info:
+                    break
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    if "cpu family" in info:
+        name += f" (family {info['cpu family']}, model {info.get('model', '?')})"
+    return name
 
 
 def cpu_baseline(torch, ref, wq, ws, K, G, x, nbytes, seconds):
@@ -664,17 +818,30 @@ def cpu_baseline(torch, ref, wq, ws, K, G, x, nbytes, seconds):
     workloads, on this host's cores: the headline cfg 1 GEMV (about half of
     `seconds`) and, under "configs", cfg 2 (decode MLP chain), cfg 4 (the
     M=1024 prefill products) and cfg 5 (lm_head + argmax, V=151,936), each
-    timed for about `seconds` / 6.  Threads: OMP_NUM_THREADS (the box's CPU
-    share), capped at the visible cores; `cores` is what torch ran with."""
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    threads = max(1, min(threads, os.cpu_count() or 1))
+    timed for about `seconds` / 6.
+
+    Threads: the GPU pool gives each GPU's job a share of the host's cores
+    (16 on a one-GPU box, exported as OMP_NUM_THREADS); os.cpu_count() there
+    counts every core of the host, most of them other jobs'.  torch runs
+    with OMP_NUM_THREADS threads, capped at the cores this process may run
+    on (its affinity set); `cores` is the count torch used, and the line
+    also states os.cpu_count() and the affinity count."""
+    ncpu = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = ncpu
+    threads = int(os.environ.get("OMP_NUM_THREADS", affinity))
+    threads = max(1, min(threads, affinity))
     torch.set_num_threads(threads)
     used = torch.get_num_threads()
     lin = ref.FakeQuantLinear(wq, ws, K, G)
     xt = torch.from_numpy(x)
     med, n = ref.time_cpu(lambda: lin(xt), warmup=3, iters=1000, max_seconds=seconds / 2)
     out = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": used, "kind": "port",
-           "cpu_model": cpu_model(),
+           "cpu_model": cpu_model(), "os_cpu_count": ncpu, "affinity_cores": affinity,
+           "threads_from": "OMP_NUM_THREADS (the pool's per-GPU core share)" if "OMP_NUM_THREADS" in os.environ
+           else "affinity set",
            "us_per_gemv": round(med * 1e6, 1),
            "sample": f"median of {n} fake-quant GEMVs (M=1 K=2048 N=6144: fq_input + fp32 x@W^T, "
                      "W dequantised once as tools/reference.py:36-40), ~%.0f s bounded" % (seconds / 2)}

@@ -60,6 +60,7 @@ extern "C" {
     pub fn wq_lm_head_argmax_noalloc(stream: *mut c_void, wq: *const u32, ws: *const u32, v: i64, k: i64,
                                      g: i32, xq: *const i8, dx: *const f32, xs: *const i32, m: i64, ga: i32,
                                      ids: *const u32, logits: *mut f32, tok_out: *mut u32) -> i32;
+    pub fn wq_lm_head_noalloc_reset(stream: *mut c_void) -> i32;
     pub fn wq_lm_head_workspace_bytes() -> usize;
     pub fn wq_workspace_clear(stream: *mut c_void, workspace: *mut c_void, bytes: usize) -> i32;
     pub fn wq_embed(stream: *mut c_void, eq: *const u32, es: *const u32, v: i64, k: i64, g: i32,

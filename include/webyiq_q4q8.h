@@ -154,6 +154,11 @@ int wq_argmax(void* stream, const float* logits, int64_t M, int64_t V,
  * wq_lm_head_workspace_bytes() bytes) carries the cross-workgroup reduction;
  * it must be zero before the first call (wq_workspace_clear) and every call
  * leaves it zero again.  Calls sharing one workspace must not overlap.
+ * The final workgroup's wait for the others is bounded (~0.5 s, far beyond
+ * any launch): if it ever runs out, every token is written as 0xFFFFFFFF
+ * (never a valid index, V <= 0xFFFFFFFE) and the workspace may be left
+ * non-zero; clear it (wq_workspace_clear, stream-ordered after the call)
+ * before the next call.
  */
 int wq_lm_head_argmax(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t V,
                       int64_t K, int32_t G, const int8_t* xq, const float* dx,
@@ -172,12 +177,23 @@ int wq_lm_head_argmax(void* stream, const uint32_t* wq, const uint32_t* ws, int6
  * Calls that overlap on one GPU (concurrent streams, or threads) race on the
  * array and must not be issued; use wq_lm_head_argmax with one workspace per
  * stream for that.  Limits: M <= 8 tokens (as wq_lm_head_argmax); other
- * arguments and the result as wq_lm_head_argmax.
+ * arguments and the result as wq_lm_head_argmax, including the 0xFFFFFFFF
+ * tokens of a wait that ran out, after which the array must be reset with
+ * wq_lm_head_noalloc_reset before the next call.
  */
 int wq_lm_head_argmax_noalloc(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t V,
                               int64_t K, int32_t G, const int8_t* xq, const float* dx,
                               const int32_t* xs, int64_t M, int32_t GA, const uint32_t* ids,
                               float* logits, uint32_t* tok_out);
+
+/*
+ * Zero the current GPU's static array of wq_lm_head_argmax_noalloc with a
+ * fill kernel on `stream` (no allocation, no hipMemset; safe inside graph
+ * capture).  No counterpart in the reference.  Needed only after a call
+ * returned 0xFFFFFFFF tokens; issue it stream-ordered after that call, with
+ * no other wq_lm_head_argmax_noalloc call in flight on the GPU.
+ */
+int wq_lm_head_noalloc_reset(void* stream);
 
 /* Bytes of workspace wq_lm_head_argmax needs (no counterpart in the
  * reference, whose argmax runs as a separate single-workgroup dispatch). */

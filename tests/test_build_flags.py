@@ -1,0 +1,70 @@
+"""The packed-fp32 guard of the HIP build (webyiq_amd/build.py CFLAGS).
+
+The library is compiled with `-Xclang -target-feature -Xclang
+-packed-fp32-ops`.  hipcc's host pass does not know that feature and says
+so; the device pass honours it.  These tests check both halves on the CPU:
+the flag removes a packed fma from a probe kernel's gfx950 code (so it is
+not ignored), and the built library's gfx950 code holds no v_pk_fma_f32,
+v_pk_mul_f32 or v_pk_add_f32.
+"""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from webyiq_amd import build as hipbuild
+
+PK = re.compile(r"\bv_pk_(fma|mul|add)_f32\b")
+OBJDUMP = "/opt/rocm/llvm/bin/llvm-objdump"
+PROBE = r"""
+#include <hip/hip_runtime.h>
+__global__ void probe(float2* a, const float2* b, const float2* c, int n) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        float2 x = a[i], y = b[i], z = c[i];
+        x.x = x.x * y.x + z.x;
+        x.y = x.y * y.y + z.y;
+        a[i] = x;
+    }
+}
+"""
+
+
+def device_asm(tmp_path, flags, tag):
+    src = tmp_path / "probe.hip"
+    src.write_text(PROBE)
+    out = tmp_path / f"probe_{tag}.s"
+    subprocess.run([hipbuild.HIPCC, "--offload-arch=gfx950", "-O3", *flags, "--cuda-device-only", "-S",
+                    str(src), "-o", str(out)], check=True, capture_output=True)
+    return out.read_text()
+
+
+@pytest.mark.skipif(not os.path.exists(hipbuild.HIPCC), reason="hipcc not installed")
+def test_flag_removes_packed_fp32_from_device_code(tmp_path):
+    flag = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+    assert all(f in hipbuild.CFLAGS for f in flag)
+    without = device_asm(tmp_path, [], "default")
+    with_flag = device_asm(tmp_path, flag, "flag")
+    assert PK.search(without), "probe no longer yields a packed fma without the flag; pick another probe"
+    assert not PK.search(with_flag)
+
+
+@pytest.mark.skipif(not (os.path.exists(hipbuild.LIB) and os.path.exists(OBJDUMP)),
+                    reason="library not built or llvm-objdump missing")
+def test_library_device_code_has_no_packed_fp32(tmp_path):
+    # llvm-objdump --offloading writes the bundles next to its input
+    lib = tmp_path / "lib.so"
+    shutil.copy(hipbuild.LIB, lib)
+    subprocess.run([OBJDUMP, "--offloading", str(lib)], check=True, capture_output=True, cwd=tmp_path)
+    objs = sorted(p for p in tmp_path.iterdir() if "amdgcn" in p.name and "gfx950" in p.name)
+    assert objs, "no gfx950 code object in the library"
+    kernels = 0
+    for o in objs:
+        asm = subprocess.run([OBJDUMP, "-d", "--mcpu=gfx950", str(o)], check=True, capture_output=True,
+                             text=True).stdout
+        kernels += asm.count(">:\n")
+        hits = PK.findall(asm)
+        assert not hits, f"{o.name}: packed fp32 ops {sorted(set(hits))}"
+    assert kernels > 0

@@ -182,6 +182,10 @@ GEMV_CASES = [
     (1, 2048, 8192, 128, None, 0),
     (2, 2048, 8192, 128, None, 2),
     (8, 1536, 7000, 128, None, 1),   # partial pass, ragged last block
+    # the o projection after the chunk merge (per-32 activations, += residual)
+    # at the decode-layer shape, 1 and 8 tokens
+    (1, 2048, 2048, 128, 32, 1),
+    (8, 2048, 2048, 128, 32, 1),
 ]
 
 
@@ -350,6 +354,28 @@ def test_gemm_prefill_sizes(M, K, N):
     assert np.all(np.isfinite(got))
 
 
+@pytest.mark.parametrize("M,mode,stride", [(2048, 0, 8), (4096, 2, 32)])
+def test_gemm_group32_wide_widths(M, mode, stride):
+    """Per-token activations at group 32 on the widths the launcher picks for
+    long prompts: 192 at M = 2048, N = 6144 (three columns per wave, the
+    columns' fragments read up front) and 256 in mode 2 at M = 4096 (four
+    columns, read column by column).  Every row of the first and the last
+    tile and one row per `stride` elsewhere (offset rotating with the tile),
+    against the oracle at rel 1e-5."""
+    K, N, G = 2048, 6144, 32
+    note(f"gemm group-32 M={M} K={K} N={N} mode={mode}")
+    rows = 2 * N if mode == 2 else N
+    wq, ws, x, xq, dx, xs = setup_linear(M + mode, M, K, rows, G, None)
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
+    got = host(ops.gemm(w, dev_acts(xq, dx, xs, K, G), mode=mode))
+    base = np.arange(0, M, stride)
+    idx = np.unique(np.concatenate([np.arange(0, 128), np.arange(M - 128, M),
+                                    base + (base // 128) % stride]))
+    want = oracle_linear_tokens(wq, ws, K, G, xq[idx], dx[idx], xs[idx], mode=mode)
+    assert rel_err(got[idx], want) < 1e-5
+    assert np.all(np.isfinite(got))
+
+
 @pytest.mark.parametrize("K,N", [(2048, 6144), (6144, 2048)])
 def test_gemm_prefill_production_int32(K, N):
     """BASELINE configs[3] on the production kernel (the tile width the
@@ -506,6 +532,19 @@ QUANT_GEMV_CASES = [
     (8, 2048, 2048, 32, 1, False),   # 8 tokens, G = 32, += residual
     (3, 128, 300, 128, 0, True),     # 3 tokens, one group, partial pass
     (6, 6144, 512, 128, 1, False),
+    # the instances the bench times (cfg 2 and the decode layers at
+    # hidden 2048, q 2048, kv 512, ffn 6144): norm+quant -> qkv (3072 rows),
+    # norm+quant -> gate_up (2 x 6144 rows), quant -> down, at 1, 2, 4, 8 tokens
+    (1, 2048, 6144, 128, 2, True),   # cfg 2 gate_up, one launch (3 rows per wave)
+    (1, 2048, 3072, 128, 0, True),
+    (2, 2048, 3072, 128, 0, True),
+    (2, 6144, 2048, 128, 1, False),
+    (4, 2048, 3072, 128, 0, True),
+    (4, 2048, 6144, 128, 2, True),
+    (4, 6144, 2048, 128, 1, False),
+    (8, 2048, 3072, 128, 0, True),
+    (8, 2048, 6144, 128, 2, True),
+    (8, 6144, 2048, 128, 1, False),
 ]
 
 
@@ -650,3 +689,39 @@ def test_decode_layer_graph_replay():
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"replay {i}"
         ops.quant(dev(rng.normal(size=(3, 256)).astype(np.float32)))   # eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+def test_decode_layer_bench_shape(M):
+    """The decode layer the bench times (hidden 2048, q 2048, kv 512, ffn
+    6144, group 128, the chunk merge in place of attention) at its token
+    counts: the fused sequence equals the unfused one (separate quantiser
+    launches) bit for bit, and its first projection (norm+quant+qkv) and the
+    o projection's merged input match the oracle."""
+    from webyiq_amd.layer import DecodeLayer
+    note(f"decode layer bench shape M={M}")
+    H, Q, KV, F, G = 2048, 2048, 512, 6144, 128
+    rng = np.random.default_rng(40 + M)
+    shapes = {"qkv": (Q + 2 * KV, H), "o": (H, Q), "gate_up": (2 * F, H), "down": (H, F)}
+    host_w = {n: ref.make_weight(rng, r, c, G) for n, (r, c) in shapes.items()}
+    w = ops.Weights({n: ops.Q4Tensor.from_numpy(q, s, shapes[n][1], G) for n, (q, s) in host_w.items()})
+    w["attn_norm"] = dev(rng.normal(1, 0.1, H).astype(np.float32))
+    w["mlp_norm"] = dev(rng.normal(1, 0.1, H).astype(np.float32))
+    x0 = dev(ref.make_activations(rng, M, H))
+    torch.manual_seed(M)
+    layer = DecodeLayer(w, M, hidden=H, q_dim=Q, kv_dim=KV, ffn=F, G=G, attention="combine")
+    plain = DecodeLayer(w, M, hidden=H, q_dim=Q, kv_dim=KV, ffn=F, G=G, fused=False, attention="combine")
+    plain.part.copy_(layer.part)
+    for lay in (layer, plain):
+        lay.x.copy_(x0)
+        lay.run()
+    got = host(layer.x)
+    assert np.array_equal(got.view(np.uint32), host(plain.x).view(np.uint32))
+    assert np.all(np.isfinite(got))
+    xq, dx, xs = orc.quant_act(host(x0), None, G, norm_w=host(w["attn_norm"]), eps=1e-6)
+    qkv_want = orc.linear(*host_w["qkv"], H, G, xq, dx, xs)
+    assert np.array_equal(host(layer.qkv).view(np.uint32), qkv_want.view(np.uint32))
+    cq, cdx, cxs = orc.attn_combine(host(layer.part), layer.pos)
+    got_q = host(layer.a_att.xq).astype(np.int32)
+    assert np.abs(got_q - cq.astype(np.int32)).max() <= 1
+    assert rel_err(host(layer.a_att.dx), cdx) < 1e-5

@@ -71,3 +71,40 @@ def test_noalloc_rejects_too_many_tokens():
                                        None, fake)
     assert rc == _lib.WQ_ESHAPE
     assert b"8" in lib.wq_last_error()
+
+
+@pytest.mark.gpu
+def test_noalloc_reset_then_calls():
+    """wq_lm_head_noalloc_reset zeroes the static array with the fill kernel
+    (stream-ordered); calls after it still give the oracle's tokens."""
+    import ctypes
+
+    import torch
+    from webyiq_amd import _lib, ops
+    lib = _lib.load()
+    print("[case] noalloc reset, then M=2 V=4096 twice", flush=True)
+    wq, ws, xq, dx, xs, _, _, tok_want = case(23, 2, 4096, False)
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
+    a = ops.Acts(*(torch.from_numpy(v).cuda() for v in (xq, dx, xs)), K, G)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.wq_lm_head_noalloc_reset(s) == _lib.WQ_OK, lib.wq_last_error()
+    t1 = ops.lm_head_argmax_noalloc(w, a)
+    assert lib.wq_lm_head_noalloc_reset(s) == _lib.WQ_OK, lib.wq_last_error()
+    t2 = ops.lm_head_argmax_noalloc(w, a)
+    torch.cuda.synchronize()
+    assert np.array_equal(t1.cpu().numpy().astype(np.uint32), tok_want)
+    assert np.array_equal(t2.cpu().numpy().astype(np.uint32), tok_want)
+
+
+def test_noalloc_reset_without_gpu_reports_error():
+    """Without a usable device the reset launches nothing and returns
+    WQ_EHIP with the runtime's message (CPU-only check)."""
+    import torch
+
+    from webyiq_amd import _lib
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present; the GPU test covers the reset")
+    lib = _lib.load()
+    rc = lib.wq_lm_head_noalloc_reset(None)
+    assert rc == _lib.WQ_EHIP
+    assert b"wq_lm_head_noalloc_reset" in lib.wq_last_error()

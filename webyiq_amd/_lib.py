@@ -43,6 +43,7 @@ PROTOTYPES = {
                           ctypes.c_int),
     "wq_lm_head_argmax_noalloc": ([_P, _P, _P, _I64, _I64, _I32, _P, _P, _P, _I64, _I32, _P, _P, _P],
                                   ctypes.c_int),
+    "wq_lm_head_noalloc_reset": ([_P], ctypes.c_int),
     "wq_lm_head_workspace_bytes": ([], _SZ),
     "wq_workspace_clear": ([_P, _P, _SZ], ctypes.c_int),
     "wq_embed": ([_P, _P, _P, _I64, _I64, _I32, _P, _I64, _P], ctypes.c_int),

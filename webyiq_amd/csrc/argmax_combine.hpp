@@ -90,9 +90,12 @@ constexpr unsigned kArgmaxSpinLimit = 1u << 22;
 // Workgroups are dispatched in index order, so each of those has been
 // dispatched to some CU when the last one runs; none waits for anything, so
 // each finishes.  The wait is bounded all the same (kArgmaxSpinLimit); if it
-// ran out, the tokens would be written as 0xFFFFFFFF, and tickets landing
-// after the clear would leave the workspace non-zero (wq_workspace_clear
-// before reusing it).
+// ran out, the tokens are written as 0xFFFFFFFF (no index has that value:
+// V <= 0xFFFFFFFE), and keys and tickets landing after the clear leave the
+// workspace non-zero.  The host then clears it before the next call
+// (wq_workspace_clear, or wq_lm_head_noalloc_reset for the library's own
+// array): once the launch has completed, every late key and ticket has
+// landed, so a stream-ordered clear leaves it zero.
 template <int MT>
 __device__ __forceinline__ void argmax_combine(const ArgmaxArgs& am, int M, int nblocks, unsigned long long best) {
     const int tid = threadIdx.x, nthreads = blockDim.x;
@@ -101,7 +104,11 @@ __device__ __forceinline__ void argmax_combine(const ArgmaxArgs& am, int M, int 
     if (!final_block && tid >= 64) return;  // only the first wave takes part
     if (tid < MT && tid < M) {
         const unsigned long long old = atomicMax(am.keys + kslot * kArgmaxSlotWords + tid, best);
-        asm volatile("" ::"v"(old));  // the returned value: this atomic has been performed
+        // The ordering point of step 2: the returned value is consumed here
+        // (the compiler waits for the atomic's return before this statement),
+        // and the "memory" clobber keeps the ticket below, an access to
+        // another address, from being moved above it.
+        asm volatile("" ::"v"(old) : "memory");
     }
     if (!final_block) {
         if (tid == 0)

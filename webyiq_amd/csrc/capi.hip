@@ -468,4 +468,12 @@ int wq_lm_head_argmax_noalloc(void* stream, const uint32_t* wq, const uint32_t* 
     return lm_head_launch(fn, stream, wq, ws, V, K, G, xq, dx, xs, M, GA, ids, logits, tok_out, p);
 }
 
+int wq_lm_head_noalloc_reset(void* stream) {
+    const char* fn = "wq_lm_head_noalloc_reset";
+    void* p = nullptr;
+    hipError_t e = scratch_ptr(&p);
+    if (e != hipSuccess) return hip_status(e, "wq_lm_head_noalloc_reset: scratch address");
+    return hip_status(wq::launch_fill_zero(p, wq::kArgmaxWorkspaceBytes, static_cast<hipStream_t>(stream)), fn);
+}
+
 }  // extern "C"
