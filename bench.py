@@ -7,11 +7,12 @@ One step = one decode GEMV launch (M=1, K=2048, N=6144, int4 group-128 weights,
 per-token int8 activations) on inputs already resident in HBM.  W warm-up
 launches, then exactly K timed launches; launch i uses weight copy i mod R
 (default R = 64 x 6.7 MB = 430 MB > the 256 MB MALL), so every launch streams
-its weights from HBM.  The K launches are captured as one HIP graph (or, with
---launch eager, issued directly) and queued behind a gate of passes over a
-512 MiB buffer, so the GPU runs them back to back with no host submission
-gap; HIP events on that stream around the K launches time the region, which
-is synchronised on both sides.
+its weights from HBM.  The W and the K launches are captured as two HIP
+graphs (or, with --launch eager, issued directly) and queued on one stream
+behind a gate of read-only passes over a 512 MiB buffer, so the GPU runs
+them back to back with no host submission gap (class Gate); HIP events on
+that stream around the K launches time the region, which is synchronised on
+both sides.
 
 Printed JSON line:
   value       whole-job GEMV throughput, algorithmic GB/s over the K steps
@@ -124,49 +125,72 @@ def graph_time(torch, launches, reps):
 
 
 class Gate:
-    """Host-independent timing of a launch sequence.  On the launch stream, a
-    gate of passes over a 512 MiB buffer (each pass reads and writes it all,
-    ~0.2 ms) runs first, long enough for the host to enqueue the whole
-    sequence behind it; then e0, the sequence, e1.  The event interval holds
-    the GPU's back-to-back launches and no host submission gap, whatever the
-    sequence length, and the gate leaves no weight copy of the sequence in
-    the 256 MB MALL.  Synchronised on both sides."""
+    """Host-independent timing of a launch sequence.  On one stream: a gate
+    of read-only passes over a 512 MiB buffer (sums; ~0.1 ms each), then the
+    warm-up launches, e0, the timed launches, e1.  The gate lasts until the
+    host has enqueued everything behind it (checked: its end event must
+    still be pending when the host is done, else the gate is doubled and the
+    run repeated), so the GPU runs the launches back to back with no host
+    submission gap, and the timed ones start in the steady state the warm-up
+    reached.  The gate leaves no weight copy in the 256 MB MALL and, being
+    read-only, no dirty lines whose write-back the timed launches would pay.
+    Synchronised on both sides."""
 
     def __init__(self, torch):
         self.torch = torch
-        self.flush = torch.zeros(128 << 20, dtype=torch.float32, device="cuda")
+        self.flush = torch.ones(128 << 20, dtype=torch.float32, device="cuda")
+        self.passes = 8
 
-    def time(self, seq, graph=True, host_us_per_launch=20.0):
-        """Seconds per launch of `seq` (callables taking a stream)."""
+    def _graph(self, seq, s):
         torch = self.torch
+        if not seq:
+            return None
+        with torch.cuda.stream(s):
+            seq[0](ctypes.c_void_p(s.cuda_stream))
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            cs = ctypes.c_void_p(s.cuda_stream)
+            for ln in seq:
+                ln(cs)
+        return g
+
+    def time(self, seq, graph=True, warm=()):
+        """Seconds per launch of `seq` (callables taking a stream), after the
+        `warm` launches on the same stream."""
+        torch = self.torch
+        warm = list(warm)
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
-        g = None
-        if graph:
-            with torch.cuda.stream(s):
-                for ln in seq[:1]:
-                    ln(ctypes.c_void_p(s.cuda_stream))
+        gw = self._graph(warm, s) if graph else None
+        gt = self._graph(seq, s) if graph else None
+        for _ in range(6):
             torch.cuda.synchronize()
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=s):
+            eg = torch.cuda.Event()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(s):
+                for _ in range(self.passes):
+                    self.flush.sum()
+                eg.record(s)
                 cs = ctypes.c_void_p(s.cuda_stream)
-                for ln in seq:
-                    ln(cs)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        passes = 2 + int(host_us_per_launch * len(seq) / 150.0)
-        with torch.cuda.stream(s):
-            for _ in range(passes):
-                self.flush.add_(1.0)
-            e0.record(s)
-            if g is not None:
-                g.replay()
-            else:
-                cs = ctypes.c_void_p(s.cuda_stream)
-                for ln in seq:
-                    ln(cs)
-            e1.record(s)
-        torch.cuda.synchronize()
+                if gw is not None:
+                    gw.replay()
+                elif not graph:
+                    for ln in warm:
+                        ln(cs)
+                e0.record(s)
+                if gt is not None:
+                    gt.replay()
+                else:
+                    for ln in seq:
+                        ln(cs)
+                e1.record(s)
+            covered = not eg.query()  # the gate still ran when the host was done
+            torch.cuda.synchronize()
+            if covered:
+                break
+            self.passes *= 2
+        self.covered = covered
         return e0.elapsed_time(e1) * 1e-3 / len(seq)
 
 
@@ -220,9 +244,9 @@ def main():
     steps, warmup = max(1, args.steps), max(0, args.warmup)
     gate = Gate(torch)
     graph = args.launch == "graph"
-    if warmup:
-        gate.time([launches[i % R] for i in range(warmup)], graph=graph)
-    t_launch = gate.time([launches[(warmup + i) % R] for i in range(steps)], graph=graph)
+    t_launch = gate.time([launches[(warmup + i) % R] for i in range(steps)], graph=graph,
+                         warm=[launches[i % R] for i in range(warmup)])
+    gate_covered = gate.covered
     nbytes = gemv_bytes(M, K, N, G)
     value = nbytes / t_launch / 1e9
     # the kernel's mean duration per launch over the timed region (HIP events
@@ -252,6 +276,7 @@ def main():
                    "bytes_per_launch": nbytes, "parallelism": "single GPU"},
         "gemv_us_per_launch": round(t_launch * 1e6, 3),
         "launch": args.launch,
+        "gate_covered_host_enqueue": gate_covered,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "parity": {"gemv_vs_oracle_bit_exact": parity},
@@ -328,7 +353,7 @@ def kernel_clock(torch, gate, launch_args, n=32):
     durs = []
     for i in range(n):
         ln = Launcher(T, "wq_gemv", list(launch_args[i % len(launch_args)]))
-        gate.time([ln], graph=False, host_us_per_launch=50.0)
+        gate.time([ln], graph=False)
         b = read_stamps(T)
         durs.append((b[:, 4].max() - b[:, 0].min()) / 100.0)
     return {"median_us": round(float(np.median(durs)), 3), "min_us": round(float(np.min(durs)), 3),
@@ -404,7 +429,7 @@ def bench_gemm(torch, lib, ops, orc, ref, args):
             sys.exit(1)
         launches = [Launcher(lib, "wq_gemm", [P(q[i].data_ptr()), P(s[i].data_ptr()), N, K, 128,
                                               P(a.xq.data_ptr()), P(a.dx.data_ptr()), P(a.xs.data_ptr()),
-                                              M, K, 0, P(ys[i].data_ptr())]) for i in range(copies)]
+                                              M, K, 0, P(ys[i].data_ptr()), None]) for i in range(copies)]
         # warm-up long enough for the clocks to settle (the first ~30-80 ms
         # of MFMA load run measurably slower), then the median of three timings
         graph_time(torch, launches, max(1, args.gemm_warmup))
@@ -681,7 +706,8 @@ def bench_configs(torch, lib, ops, orc):
     a = ops.quant(torch.randn((M, K), dtype=torch.float32, device="cuda"), G=32)
     ys = [torch.empty((M, N), dtype=torch.float32, device="cuda") for _ in range(8)]
     launches = [Launcher(lib, "wq_gemm", [P(q.data_ptr()), P(sc.data_ptr()), N, K, 32, P(a.xq.data_ptr()),
-                                          P(a.dx.data_ptr()), P(a.xs.data_ptr()), M, K, 0, P(ys[i].data_ptr())])
+                                          P(a.dx.data_ptr()), P(a.xs.data_ptr()), M, K, 0, P(ys[i].data_ptr()),
+                                          None])
                 for i, (q, sc) in enumerate(ws)]
     graph_time(torch, launches, 50)
     t = graph_time(torch, launches, 10)
@@ -715,7 +741,8 @@ def bench_configs(torch, lib, ops, orc):
             parts.append(pt)
         a = ops.empty_acts(M, Hh * Dh, 32, G)
         lns = [Launcher(lib, "wq_attn_combine", [P(pt.data_ptr()), M, Hh, Dh, nch, pos, None, 0,
-                                                 P(a.xq.data_ptr()), P(a.dx.data_ptr()), P(a.xs.data_ptr())])
+                                                 P(a.xq.data_ptr()), P(a.dx.data_ptr()), P(a.xs.data_ptr()),
+                                                 None])
                for pt in parts]
         graph_time(torch, lns, 2)
         t = graph_time(torch, lns, 16)

@@ -19,7 +19,7 @@
 
 use std::ffi::{c_char, c_void, CStr};
 
-pub const WQ_ABI_VERSION: i32 = 1;
+pub const WQ_ABI_VERSION: i32 = 2;
 
 pub const WQ_OK: i32 = 0;
 pub const WQ_EINVAL: i32 = -1;
@@ -36,6 +36,19 @@ pub const WQ_PATH_DECODE: i32 = 0;
 pub const WQ_PATH_SPEC: i32 = 1;
 pub const WQ_PATH_PREFILL: i32 = 2;
 
+/// The step parameters the kernels read when they run (`wq_params`; the
+/// engine's `Params` uniform, gemm_q4q8.wgsl:8-13), passed as a pointer to
+/// device memory: the engine's `params` buffer (graph.rs:413-416), written
+/// per step by the host (lib.rs:312-314) or by the GPU (lib.rs:325).
+#[repr(C)]
+#[derive(Clone, Copy, Debug, Default)]
+pub struct WqParams {
+    pub pos: u32,
+    pub seq_len: u32,
+    pub m: u32,
+    pub slot: u32,
+}
+
 extern "C" {
     pub fn wq_last_error() -> *const c_char;
     pub fn wq_abi_version() -> i32;
@@ -47,10 +60,11 @@ extern "C" {
                          ws: *const u32, n: i64, k: i64, g: i32, m: i64, mode: i32, xq: *mut i8, dx: *mut f32,
                          xs: *mut i32, y: *mut f32) -> i32;
     pub fn wq_gemm(stream: *mut c_void, wq: *const u32, ws: *const u32, n: i64, k: i64, g: i32, xq: *const i8,
-                   dx: *const f32, xs: *const i32, m: i64, ga: i32, mode: i32, y: *mut f32) -> i32;
+                   dx: *const f32, xs: *const i32, m: i64, ga: i32, mode: i32, y: *mut f32,
+                   params: *const WqParams) -> i32;
     pub fn wq_matmul(stream: *mut c_void, path: i32, wq: *const u32, ws: *const u32, n: i64, k: i64, g: i32,
                      xq: *const i8, dx: *const f32, xs: *const i32, m: i64, ga: i32, mode: i32,
-                     y: *mut f32) -> i32;
+                     y: *mut f32, params: *const WqParams) -> i32;
     pub fn wq_argmax(stream: *mut c_void, logits: *const f32, m: i64, v: i64, ids: *const u32,
                      tok_out: *mut u32) -> i32;
     pub fn wq_lm_head_argmax(stream: *mut c_void, wq: *const u32, ws: *const u32, v: i64, k: i64, g: i32,
@@ -71,7 +85,8 @@ extern "C" {
                      norm_e: *const f32, norm_h: *const f32, eps: f32, m: i64, k: i64, xq: *mut i8,
                      dx: *mut f32, xs: *mut i32) -> i32;
     pub fn wq_attn_combine(stream: *mut c_void, part: *const f32, m: i64, h: i64, d: i64, nch: i64, pos: i64,
-                           gate: *const f32, gate_stride: i64, xq: *mut i8, dx: *mut f32, xs: *mut i32) -> i32;
+                           gate: *const f32, gate_stride: i64, xq: *mut i8, dx: *mut f32, xs: *mut i32,
+                           params: *const WqParams) -> i32;
     pub fn wq_gemv_debug_acc(stream: *mut c_void, wq: *const u32, ws: *const u32, n: i64, k: i64, g: i32,
                              xq: *const i8, dx: *const f32, xs: *const i32, m: i64, ga: i32, mode: i32,
                              y: *mut f32, acc: *mut i32) -> i32;
@@ -137,12 +152,15 @@ pub unsafe fn gemv(st: Stream, w: &Q4Weight, n: i64, a: &Acts, mode: i32, y: *mu
     check(wq_gemv(st.0, w.q, w.s, n, w.k, w.g, a.xq, a.dx, a.xs, a.m, a.ga, mode, y))
 }
 
-/// `Builder::gemm`: prefill GEMM on int8 MFMA, any token count.
+/// `Builder::gemm`: prefill GEMM on int8 MFMA, any token count.  With a
+/// non-null `params` (the engine's params buffer), `a.m` is the capacity and
+/// the kernel covers `params.m` tokens, read when it runs.
 ///
 /// # Safety
 /// All pointers must be device memory of the documented sizes.
-pub unsafe fn gemm(st: Stream, w: &Q4Weight, n: i64, a: &Acts, mode: i32, y: *mut f32) -> Result<(), String> {
-    check(wq_gemm(st.0, w.q, w.s, n, w.k, w.g, a.xq, a.dx, a.xs, a.m, a.ga, mode, y))
+pub unsafe fn gemm(st: Stream, w: &Q4Weight, n: i64, a: &Acts, mode: i32, y: *mut f32,
+                   params: *const WqParams) -> Result<(), String> {
+    check(wq_gemm(st.0, w.q, w.s, n, w.k, w.g, a.xq, a.dx, a.xs, a.m, a.ga, mode, y, params))
 }
 
 /// `Builder::matmul`: the engine's `Path` picks the GEMV or the GEMM.
@@ -150,8 +168,8 @@ pub unsafe fn gemm(st: Stream, w: &Q4Weight, n: i64, a: &Acts, mode: i32, y: *mu
 /// # Safety
 /// All pointers must be device memory of the documented sizes.
 pub unsafe fn matmul(st: Stream, path: i32, w: &Q4Weight, n: i64, a: &Acts, mode: i32,
-                     y: *mut f32) -> Result<(), String> {
-    check(wq_matmul(st.0, path, w.q, w.s, n, w.k, w.g, a.xq, a.dx, a.xs, a.m, a.ga, mode, y))
+                     y: *mut f32, params: *const WqParams) -> Result<(), String> {
+    check(wq_matmul(st.0, path, w.q, w.s, n, w.k, w.g, a.xq, a.dx, a.xs, a.m, a.ga, mode, y, params))
 }
 
 /// A quant -> decode matmul pair of the layer in one call (one launch for

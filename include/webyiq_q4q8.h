@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define WQ_ABI_VERSION 1
+#define WQ_ABI_VERSION 2
 
 /* status codes */
 #define WQ_OK 0
@@ -56,6 +56,25 @@ extern "C" {
 #define WQ_MODE_STORE 0
 #define WQ_MODE_ACCUMULATE 1
 #define WQ_MODE_SILU_MUL 2
+
+/*
+ * Step parameters read by the kernels at run time, the reference's Params
+ * uniform (gemm_q4q8.wgsl:8-13, attn_combine.wgsl:6-11; written by the host
+ * per step, lib.rs:312-314, or by the GPU itself on the speculative path,
+ * lib.rs:325).  Passed as a pointer to 16 bytes of device memory, so a
+ * recorded call (HIP graph, replayed op list) follows whatever the buffer
+ * holds when the kernel runs.
+ *   pos      position of the step's first token
+ *   seq_len  attention length (not read by this library's kernels)
+ *   m        tokens in the step
+ *   slot     readback slot (not read by this library's kernels)
+ */
+typedef struct wq_params {
+    uint32_t pos;
+    uint32_t seq_len;
+    uint32_t m;
+    uint32_t slot;
+} wq_params;
 
 /* which dispatch list a product belongs to (graph.rs:127-146 Path) */
 #define WQ_PATH_DECODE 0  /* one token: GEMV */
@@ -117,25 +136,34 @@ int wq_quant_gemv(void* stream, const float* x, const float* norm_w, float eps,
 
 /*
  * Prefill GEMM, any M >= 1 (tiles of 128 tokens).  Replaces Builder::gemm
- * (graph.rs:200-205) and gemm_q4q8.wgsl:46-121.  Same arguments and
- * constraints as wq_gemv, plus M * K and rows * K / 2 (rows = N, or 2N in
- * WQ_MODE_SILU_MUL) below 4 GiB.  The int32 group sums are the GEMV's; with
- * per-token activations (G = 128 or 32) the min term is summed on an f16
- * MFMA (exact products, fp32 sums in hardware order) and per-32 activations
- * fold one chain per output (the GEMV: chains and a tree): the fp32 outputs
- * agree with wq_gemv within rel 1e-5.
+ * (graph.rs:200-205, which binds the step's Params) and
+ * gemm_q4q8.wgsl:46-121.  Same arguments and constraints as wq_gemv, plus
+ * M * K and rows * K / 2 (rows = N, or 2N in WQ_MODE_SILU_MUL) below 4 GiB.
+ * params (device memory, nullable): NULL -> the product covers M tokens.
+ * Otherwise M is the capacity the launch is sized for (xq, dx, xs and y hold
+ * M rows) and the kernel reads params->m when it runs: tokens
+ * 0 .. min(params->m, M) - 1 are computed and stored, rows past them are
+ * neither read beyond row M - 1 nor written, and token tiles past them end at
+ * once (the reference clamps its tokens to p.m, gemm_q4q8.wgsl:69,106).
+ * The int32 group sums are the GEMV's; with per-token activations (G = 128
+ * or 32) the min term is summed on an f16 MFMA (exact products, fp32 sums in
+ * hardware order) and per-32 activations fold one chain per output (the
+ * GEMV: chains and a tree): the fp32 outputs agree with wq_gemv within
+ * rel 1e-5.
  */
 int wq_gemm(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K,
             int32_t G, const int8_t* xq, const float* dx, const int32_t* xs,
-            int64_t M, int32_t GA, int32_t mode, float* y);
+            int64_t M, int32_t GA, int32_t mode, float* y, const wq_params* params);
 
 /*
- * Builder::matmul (graph.rs:207-214): WQ_PATH_PREFILL -> wq_gemm, otherwise
- * wq_gemv (WQ_PATH_DECODE requires M == 1, WQ_PATH_SPEC M <= 8).
+ * Builder::matmul (graph.rs:207-214): WQ_PATH_PREFILL -> wq_gemm (with
+ * params, nullable), otherwise wq_gemv (WQ_PATH_DECODE requires M == 1,
+ * WQ_PATH_SPEC M <= 8; params unused, as the reference's gemv binds none).
  */
 int wq_matmul(void* stream, int32_t path, const uint32_t* wq, const uint32_t* ws,
               int64_t N, int64_t K, int32_t G, const int8_t* xq, const float* dx,
-              const int32_t* xs, int64_t M, int32_t GA, int32_t mode, float* y);
+              const int32_t* xs, int64_t M, int32_t GA, int32_t mode, float* y,
+              const wq_params* params);
 
 /*
  * Greedy argmax over logits f32 [M, V] (argmax.wgsl:14-43): the maximum over
@@ -249,10 +277,15 @@ int wq_mtp_in(void* stream, const float* emb, const float* x, const float* norm_
  * and the output is divided by 1 + exp(-gate).  xq i8 [M, H*D],
  * dx f32 [M, H*D/32], xs i32 [M, H*D/32]; D in {64, 128, 256},
  * nch <= 8192, pos + M - 1 < 32 nch; xq 16-byte aligned.
+ * params (device memory, nullable): when set, the position is read at run
+ * time from params->pos, as the reference counts its chunks from p.pos
+ * (attn_combine.wgsl:24,35), and the host `pos` is the largest position the
+ * call may see: a device value above it is clamped to it, so no chunk past
+ * nch is read.
  */
 int wq_attn_combine(void* stream, const float* part, int64_t M, int64_t H, int64_t D,
                     int64_t nch, int64_t pos, const float* gate, int64_t gate_stride,
-                    int8_t* xq, float* dx, int32_t* xs);
+                    int8_t* xq, float* dx, int32_t* xs, const wq_params* params);
 
 /*
  * Test hooks: wq_gemv / wq_gemm that also store the exact int32 group sums

@@ -130,7 +130,7 @@ static void cpu_checks() {
     auto op = bo.gemv("up_proj", "mlp.up", K, N, 0, 1, a, y);
     CHECK(op.is_ok(), "misaligned op still builds");
     int later = 0;
-    std::vector<OpDef> ops{op.value(), OpDef{"after", [&](void*) { ++later; return WQ_OK; }}};
+    std::vector<OpDef> ops{op.value(), OpDef{"after", [&](void*, Step) { ++later; return WQ_OK; }}};
     auto r = encode(ops, nullptr);
     CHECK(!r.is_ok(), "encode reports the rejected op");
     if (!r.is_ok())
@@ -159,9 +159,24 @@ static void cpu_checks() {
     expect_err(b.mtp_in("mtp_in", K / 2, 1e-6, x, x, half, half, half, 2, a), "per-32", "mtp_in ga");
     expect_err(b.mtp_in("mtp_in", K / 2, 1e-6, x, x, half, half, fake(0xA0000, 8), 2, p32), "norm_h holds", "norm_h");
 
-    std::vector<OpDef> fine{OpDef{"a", [&](void*) { ++later; return WQ_OK; }},
-                            OpDef{"b", [&](void*) { ++later; return WQ_OK; }}};
+    std::vector<OpDef> fine{OpDef{"a", [&](void*, Step) { ++later; return WQ_OK; }},
+                            OpDef{"b", [&](void*, Step) { ++later; return WQ_OK; }}};
     CHECK(encode(fine, nullptr).is_ok() && later == 2, "encode runs every op in order");
+    // encode hands every op the step it replays (Engine::resolve's seq_len, m)
+    uint32_t seen_m = 0, seen_len = 0;
+    std::vector<OpDef> stepped{OpDef{"s", [&](void*, Step st) {
+        seen_m = st.m;
+        seen_len = st.seq_len;
+        return WQ_OK;
+    }}};
+    CHECK(encode(stepped, nullptr, Step{300, 77}).is_ok() && seen_m == 77 && seen_len == 300,
+          "encode passes the step to its ops");
+    // the Params buffer is 16 bytes of device memory
+    const Buffer small_params = fake(0xF0000, 8);
+    expect_err(b.gemm("gemm", "mlp.up", K, N, 0, 8, a, y, &small_params), "gemm: params holds 8 bytes",
+               "params size");
+    expect_err(b.attn_combine("combine", part, 2, 2, 128, 4, 100, nullptr, 0, p32, &small_params),
+               "combine: params holds 8 bytes", "combine params size");
 }
 
 // ---------------------------------------------------------------- GPU mode
@@ -423,6 +438,108 @@ static void gpu_producers() {
     std::fflush(stdout);
 }
 
+// Device step parameters (wq_params): a prefill chunk's list recorded for
+// 128 tokens runs the m tokens the Params buffer holds when it replays, and a
+// chunk-merge op recorded once follows the position written into the buffer,
+// each against the oracle; the host-resolved step (encode's Step) sizes the
+// same ops without the buffer.
+static void gpu_params() {
+    const uint32_t H = 1024, N = 512, CAP = kPrefillChunk;
+    const int G = 128;
+    std::mt19937 rng(91);
+    Q4Host w = make_weight(rng, N, H, G);
+    Dev d;
+    Builder b({{"w.q", d.put(w.q)}, {"w.s", d.put(w.s)}}, G);
+    std::normal_distribution<float> nd(0.0f, 1.0f);
+    std::vector<float> x((size_t)CAP * H);
+    for (float& v : x) v = nd(rng);
+    const Buffer xr = d.put(x);
+    Acts a;
+    a.xq = d.zeros((size_t)CAP * H);
+    a.dx = d.zeros((size_t)CAP * 4);
+    a.xs = d.zeros((size_t)CAP * (H / G) * 4);
+    const std::vector<float> sentinel((size_t)CAP * N, std::nanf(""));
+    const Buffer y = d.put(sentinel);
+    wq_params hp{0, 0, CAP, 0};
+    const Buffer prm = d.put(std::vector<wq_params>{hp});
+
+    std::vector<OpDef> ops;
+    auto add = [&](std::vector<OpDef>& list, Result<OpDef> r) {
+        CHECK(r.is_ok(), "build: %s", r.error().c_str());
+        if (r.is_ok()) list.push_back(r.value());
+    };
+    add(ops, b.quant("quant", H, 1e-6, xr, nullptr, CAP, a));
+    add(ops, b.matmul(Path::Prefill, "gemm", "w", H, N, WQ_MODE_STORE, a, y, CAP, &prm));
+    // oracle over all 128 tokens (the quantiser runs per token)
+    std::vector<int8_t> q((size_t)CAP * H);
+    std::vector<float> dx(CAP), want((size_t)CAP * N);
+    std::vector<int32_t> xs((size_t)CAP * (H / G));
+    or_quant_act(x.data(), nullptr, 1e-6f, CAP, H, (int)H, G, q.data(), dx.data(), xs.data());
+    or_linear(w.q.data(), w.s.data(), N, H, G, q.data(), dx.data(), xs.data(), CAP, (int)H, 0, want.data());
+    auto rows_match = [&](const std::vector<float>& got, uint32_t m) {
+        std::vector<float> g0(got.begin(), got.begin() + (size_t)m * N), w0(want.begin(), want.begin() + (size_t)m * N);
+        bool rest_untouched = true;
+        for (size_t i = (size_t)m * N; i < got.size(); ++i) rest_untouched &= std::isnan(got[i]);
+        return std::make_pair(rel_err(g0, w0), rest_untouched);
+    };
+    for (uint32_t m : {77u, 128u, 1u}) {
+        HIP_OK(hipMemcpy(y.ptr, sentinel.data(), sentinel.size() * 4, hipMemcpyHostToDevice));
+        hp.m = m;
+        HIP_OK(hipMemcpy(prm.ptr, &hp, sizeof hp, hipMemcpyHostToDevice));  // only the Params buffer changes
+        auto r = encode(ops, nullptr);
+        CHECK(r.is_ok(), "encode: %s", r.error().c_str());
+        HIP_OK(hipDeviceSynchronize());
+        auto [e, untouched] = rows_match(get<float>(y, sentinel.size()), m);
+        CHECK(e < 1e-5 && untouched, "params m=%u: rows 0..m-1 rel err %.3g, rows past m untouched %d", m, e,
+              (int)untouched);
+    }
+    // the host-resolved step sizes the same ops (params left at 128)
+    hp.m = CAP;
+    HIP_OK(hipMemcpy(prm.ptr, &hp, sizeof hp, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(y.ptr, sentinel.data(), sentinel.size() * 4, hipMemcpyHostToDevice));
+    auto r = encode(ops, nullptr, Step{0, 50});
+    CHECK(r.is_ok(), "encode step: %s", r.error().c_str());
+    HIP_OK(hipDeviceSynchronize());
+    auto [e50, u50] = rows_match(get<float>(y, sentinel.size()), 50);
+    CHECK(e50 < 1e-5 && u50, "Step m=50: rel err %.3g, rows past m untouched %d", e50, (int)u50);
+
+    // chunk merge recorded once, replayed at three positions
+    const uint32_t HH = 4, D = 128, NCH = 16, T = 2;
+    const int64_t BOUND = 32 * NCH - T;
+    std::normal_distribution<float> pn(0.0f, 3.0f);
+    std::uniform_real_distribution<float> ud(1.0f, 32.0f);
+    std::vector<float> part((size_t)T * HH * NCH * (D + 2));
+    for (size_t i = 0; i < part.size(); ++i) {
+        const size_t c = i % (D + 2);
+        part[i] = c == D ? 0.75f : c == D + 1 ? ud(rng) : pn(rng);
+    }
+    Acts ao;
+    ao.xq = d.zeros((size_t)T * HH * D);
+    ao.dx = d.zeros((size_t)T * HH * D / 32 * 4);
+    ao.xs = d.zeros((size_t)T * HH * D / 32 * 4);
+    ao.ga = 32;
+    std::vector<OpDef> comb;
+    add(comb, b.attn_combine("attn_combine", d.put(part), T, HH, D, NCH, BOUND, nullptr, 0, ao, &prm));
+    for (uint32_t pos : {40u, 300u, 7u}) {
+        hp.pos = pos;
+        HIP_OK(hipMemcpy(prm.ptr, &hp, sizeof hp, hipMemcpyHostToDevice));
+        auto rc = encode(comb, nullptr);
+        CHECK(rc.is_ok(), "encode combine: %s", rc.error().c_str());
+        HIP_OK(hipDeviceSynchronize());
+        const uint32_t KO = HH * D;
+        std::vector<int8_t> cq((size_t)T * KO);
+        std::vector<float> cd((size_t)T * KO / 32);
+        std::vector<int32_t> cs((size_t)T * KO / 32);
+        or_attn_combine(part.data(), T, HH, D, NCH, pos, nullptr, 0, cq.data(), cd.data(), cs.data());
+        CHECK(same_bits(get<int8_t>(ao.xq, cq.size()), cq) && same_bits(get<float>(ao.dx, cd.size()), cd) &&
+                  same_bits(get<int32_t>(ao.xs, cs.size()), cs),
+              "params pos=%u: attn_combine codes, scales, sums", pos);
+    }
+    std::printf("  params: prefill list for 128 tokens at m = 77, 128, 1 and Step m = 50; "
+                "chunk merge at positions 40, 300, 7: compared with the oracle\n");
+    std::fflush(stdout);
+}
+
 static void gpu_checks() {
     int n = 0;
     HIP_OK(hipGetDeviceCount(&n));
@@ -434,6 +551,7 @@ static void gpu_checks() {
     gpu_step(Path::Spec, 2);
     gpu_step(Path::Prefill, 128);
     gpu_producers();
+    gpu_params();
 }
 
 int main(int argc, char** argv) {

@@ -25,14 +25,15 @@ def test_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(_lib.PROTOTYPES)
-    assert L.wq_abi_version() == 1
+    assert L.wq_abi_version() == 2
     assert L.wq_lm_head_workspace_bytes() >= 72
 
 
 def gemv(*, wq=A16, ws=A4, N=64, K=2048, G=128, xq=A16, dx=A4, xs=A4, M=1, GA=None, mode=0, y=A4,
-         fn="wq_gemv"):
+         fn="wq_gemv", params=None):
     GA = K if GA is None else GA
-    return getattr(L, fn)(None, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y)
+    extra = [params] if fn == "wq_gemm" else []
+    return getattr(L, fn)(None, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, *extra)
 
 
 def err():
@@ -63,10 +64,12 @@ def test_gemv_token_and_k_limits():
     # ... while each operand stays within 4 GiB of 32-bit staging offsets
     assert gemv(M=1 << 20, K=8192, fn="wq_gemm") == _lib.WQ_ESHAPE and "4 GiB" in err()
     assert gemv(N=1 << 20, K=8192, mode=2, fn="wq_gemm") == _lib.WQ_ESHAPE
+    # the step parameters are device words read by the kernel: 4-byte aligned
+    assert gemv(params=ctypes.c_void_p(0x10002), fn="wq_gemm") == _lib.WQ_EALIGN and "params" in err()
 
 
 def test_matmul_paths():
-    args = [A16, A4, 64, 2048, 128, A16, A4, A4, 2, 2048, 0, A4]
+    args = [A16, A4, 64, 2048, 128, A16, A4, A4, 2, 2048, 0, A4, None]
     assert L.wq_matmul(None, 7, *args) == _lib.WQ_EINVAL and "unknown path" in err()
     assert L.wq_matmul(None, _lib.PATH_DECODE, *args) == _lib.WQ_ESHAPE and "M = 1" in err()
 
@@ -146,8 +149,8 @@ def test_mtp_in_argument_errors():
     assert mtp_in(xq=ctypes.c_void_p(0x10008)) == _lib.WQ_EALIGN
 
 
-def combine(*, part=A4, M=1, H=16, D=128, nch=128, pos=0, gate=None, gs=0, xq=A16, dx=A4, xs=A4):
-    return L.wq_attn_combine(None, part, M, H, D, nch, pos, gate, gs, xq, dx, xs)
+def combine(*, part=A4, M=1, H=16, D=128, nch=128, pos=0, gate=None, gs=0, xq=A16, dx=A4, xs=A4, params=None):
+    return L.wq_attn_combine(None, part, M, H, D, nch, pos, gate, gs, xq, dx, xs, params)
 
 
 def test_attn_combine_argument_errors():
@@ -161,6 +164,9 @@ def test_attn_combine_argument_errors():
     assert combine(gate=A4, gs=2 * 16 * 128 - 1) == _lib.WQ_ESHAPE and "gate_stride" in err()
     assert combine(xq=ctypes.c_void_p(0x10008)) == _lib.WQ_EALIGN
     assert combine(part=ctypes.c_void_p(0x10002)) == _lib.WQ_EALIGN
+    # with device params the host pos is the bound: it is checked the same way
+    assert combine(nch=4, pos=128, params=A4) == _lib.WQ_ESHAPE and "context" in err()
+    assert combine(params=ctypes.c_void_p(0x10002)) == _lib.WQ_EALIGN and "params" in err()
 
 
 def test_last_error_is_per_thread():

@@ -20,6 +20,7 @@ C_TO_RUST = {
     "int32_t": "i32", "int32_t*": "*mut i32", "const int32_t*": "*const i32",
     "uint32_t*": "*mut u32", "const uint32_t*": "*const u32",
     "int64_t": "i64", "size_t": "usize", "int": "i32",
+    "const wq_params*": "*const WqParams",
 }
 
 
@@ -88,6 +89,18 @@ def test_constants_match_the_header():
     assert defs and set(defs) == set(consts)
     for k, v in defs.items():
         assert int(consts[k]) == int(v), k
+
+
+def test_params_struct_matches_the_header():
+    """wq_params and the crate's #[repr(C)] WqParams: the same u32 fields in
+    the same order (the layout the kernels read, word 0 pos, word 2 m)."""
+    hdr = _strip_c_comments(open(HEADER).read())
+    cfields = re.findall(r"uint32_t\s+(\w+);", re.search(r"typedef struct wq_params \{(.*?)\}", hdr, re.S).group(1))
+    text = open(os.path.join(CRATE, "src", "lib.rs")).read()
+    body = re.search(r"#\[repr\(C\)\][^{]*pub struct WqParams \{(.*?)\}", text, re.S).group(1)
+    rfields = re.findall(r"pub (\w+): u32,", body)
+    assert cfields == ["pos", "seq_len", "m", "slot"]
+    assert rfields == cfields
 
 
 def test_header_parser_catches_a_mismatch():

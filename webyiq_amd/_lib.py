@@ -34,10 +34,10 @@ PROTOTYPES = {
     "wq_quant_act": ([_P, _P, _P, _F, _I64, _I64, _I32, _I32, _P, _P, _P], ctypes.c_int),
     "wq_gemv": (_LINEAR, ctypes.c_int),
     "wq_quant_gemv": ([_P, _P, _P, _F, _P, _P, _I64, _I64, _I32, _I64, _I32, _P, _P, _P, _P], ctypes.c_int),
-    "wq_gemm": (_LINEAR, ctypes.c_int),
+    "wq_gemm": (_LINEAR + [_P], ctypes.c_int),
     "wq_gemv_debug_acc": (_LINEAR + [_P], ctypes.c_int),
     "wq_gemm_debug_acc": (_LINEAR + [_P], ctypes.c_int),
-    "wq_matmul": ([_P, _I32] + _LINEAR[1:], ctypes.c_int),
+    "wq_matmul": ([_P, _I32] + _LINEAR[1:] + [_P], ctypes.c_int),
     "wq_argmax": ([_P, _P, _I64, _I64, _P, _P], ctypes.c_int),
     "wq_lm_head_argmax": ([_P, _P, _P, _I64, _I64, _I32, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _SZ],
                           ctypes.c_int),
@@ -49,7 +49,7 @@ PROTOTYPES = {
     "wq_embed": ([_P, _P, _P, _I64, _I64, _I32, _P, _I64, _P], ctypes.c_int),
     "wq_gather_rows": ([_P, _P, _P, _I64, _I64, _I32, _P, _I64, _P, _P], ctypes.c_int),
     "wq_mtp_in": ([_P, _P, _P, _P, _P, _P, _F, _I64, _I64, _P, _P, _P], ctypes.c_int),
-    "wq_attn_combine": ([_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _P], ctypes.c_int),
+    "wq_attn_combine": ([_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P], ctypes.c_int),
 }
 
 

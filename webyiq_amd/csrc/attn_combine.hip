@@ -53,7 +53,7 @@ __device__ __forceinline__ int group_sum(int v) {
 
 template <int DPL>
 __global__ __launch_bounds__(64 * kCombineWaves) void attn_combine_kernel(AttnCombineArgs a) {
-    pin_arg(a.part); pin_arg(a.M); pin_arg(a.H); pin_arg(a.nch); pin_arg(a.pos);
+    pin_arg(a.part); pin_arg(a.M); pin_arg(a.H); pin_arg(a.nch); pin_arg(a.pos); pin_arg(a.params);
     pin_arg(a.gate); pin_arg(a.gate_stride); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
     constexpr int D = 64 * DPL;
     constexpr int LPG = 32 / DPL;  // lanes per 32-dim group
@@ -63,7 +63,14 @@ __global__ __launch_bounds__(64 * kCombineWaves) void attn_combine_kernel(AttnCo
     const int64_t item = blockIdx.x;  // m * H + h
     const int64_t m = item / a.H, h = item - m * a.H;
     const int nch = (int)a.nch;
-    const int n = (int)((a.pos + m + kChunk) / kChunk);  // <= nch (checked on the host)
+    // the step's position: the host's, or the device Params' (clamped to the
+    // host bound, so that n <= nch whatever the buffer holds)
+    int64_t pos = a.pos;
+    if (a.params) {
+        const int64_t p = (int64_t)a.params[kParamPos];
+        pos = p < a.pos ? p : a.pos;
+    }
+    const int n = (int)((pos + m + kChunk) / kChunk);  // <= nch (checked on the host)
     const float* hb = a.part + item * (int64_t)nch * (D + 2);
     float* w = sh;
     float* chains = sh + nch;

@@ -138,7 +138,8 @@ int check_gemv_shape(const char* fn, int64_t M, int64_t K) {
 
 wq::LinearArgs make_args(const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K, int32_t G,
                          const int8_t* xq, const float* dx, const int32_t* xs, int64_t M,
-                         int32_t GA, int32_t mode, float* y, int32_t* acc) {
+                         int32_t GA, int32_t mode, float* y, int32_t* acc,
+                         const wq_params* params = nullptr) {
     wq::LinearArgs a{};
     a.wq = wq;
     a.ws = ws;
@@ -153,6 +154,7 @@ wq::LinearArgs make_args(const uint32_t* wq, const uint32_t* ws, int64_t N, int6
     a.mode = mode;
     a.y = y;
     a.acc_dump = acc;
+    a.params = reinterpret_cast<const uint32_t*>(params);
     return a;
 }
 
@@ -169,7 +171,8 @@ int gemv_impl(const char* fn, void* stream, const uint32_t* wq, const uint32_t* 
 
 int gemm_impl(const char* fn, void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N,
               int64_t K, int32_t G, const int8_t* xq, const float* dx, const int32_t* xs,
-              int64_t M, int32_t GA, int32_t mode, float* y, int32_t* acc) {
+              int64_t M, int32_t GA, int32_t mode, float* y, int32_t* acc,
+              const wq_params* params = nullptr) {
     int rc = check_linear(fn, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, true);
     if (rc) return rc;
     // the GEMM stages tiles with 32-bit byte offsets from each operand's base
@@ -178,7 +181,8 @@ int gemm_impl(const char* fn, void* stream, const uint32_t* wq, const uint32_t* 
     if (M * K > lim || rows * (K / 2) > lim)
         return fail(WQ_ESHAPE, "%s: M = %lld, rows = %lld, K = %lld address more than 4 GiB of one operand; "
                     "split the call along M or N", fn, (long long)M, (long long)rows, (long long)K);
-    auto a = make_args(wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, acc);
+    if (params) REQUIRE_ALIGN(params, 4);
+    auto a = make_args(wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, acc, params);
     return hip_status(wq::launch_gemm(a, static_cast<hipStream_t>(stream)), fn);
 }
 
@@ -244,8 +248,8 @@ int wq_quant_gemv(void* stream, const float* x, const float* norm_w, float eps, 
 
 int wq_gemm(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K, int32_t G,
             const int8_t* xq, const float* dx, const int32_t* xs, int64_t M, int32_t GA,
-            int32_t mode, float* y) {
-    return gemm_impl("wq_gemm", stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, nullptr);
+            int32_t mode, float* y, const wq_params* params) {
+    return gemm_impl("wq_gemm", stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, nullptr, params);
 }
 
 int wq_gemv_debug_acc(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K,
@@ -266,11 +270,11 @@ int wq_gemm_debug_acc(void* stream, const uint32_t* wq, const uint32_t* ws, int6
 
 int wq_matmul(void* stream, int32_t path, const uint32_t* wq, const uint32_t* ws, int64_t N,
               int64_t K, int32_t G, const int8_t* xq, const float* dx, const int32_t* xs,
-              int64_t M, int32_t GA, int32_t mode, float* y) {
+              int64_t M, int32_t GA, int32_t mode, float* y, const wq_params* params) {
     const char* fn = "wq_matmul";
     switch (path) {
         case WQ_PATH_PREFILL:
-            return gemm_impl(fn, stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, nullptr);
+            return gemm_impl(fn, stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, nullptr, params);
         case WQ_PATH_DECODE:
             if (M != 1) return fail(WQ_ESHAPE, "%s: decode path takes M = 1, got %lld", fn, (long long)M);
             return gemv_impl(fn, stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, nullptr);
@@ -370,7 +374,7 @@ int wq_mtp_in(void* stream, const float* emb, const float* x, const float* norm_
 
 int wq_attn_combine(void* stream, const float* part, int64_t M, int64_t H, int64_t D, int64_t nch,
                     int64_t pos, const float* gate, int64_t gate_stride, int8_t* xq, float* dx,
-                    int32_t* xs) {
+                    int32_t* xs, const wq_params* params) {
     const char* fn = "wq_attn_combine";
     REQUIRE_PTR(part);
     REQUIRE_PTR(xq);
@@ -394,7 +398,9 @@ int wq_attn_combine(void* stream, const float* part, int64_t M, int64_t H, int64
     REQUIRE_ALIGN(xq, 16);
     REQUIRE_ALIGN(dx, 4);
     REQUIRE_ALIGN(xs, 4);
-    wq::AttnCombineArgs a{part, M, H, D, nch, pos, gate, gate_stride, xq, dx, xs};
+    if (params) REQUIRE_ALIGN(params, 4);
+    wq::AttnCombineArgs a{part, M, H, D, nch, pos, reinterpret_cast<const uint32_t*>(params), gate,
+                          gate_stride, xq, dx, xs};
     return hip_status(wq::launch_attn_combine(a, static_cast<hipStream_t>(stream)), fn);
 }
 

@@ -198,7 +198,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
 
     const LinearArgs& a = p.a;
     pin_arg(a.wq); pin_arg(a.ws); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs); pin_arg(a.y);
-    pin_arg(a.N); pin_arg(a.K); pin_arg(a.M);
+    pin_arg(a.N); pin_arg(a.K); pin_arg(a.M); pin_arg(a.params);
     pin_arg(p.tilesM); pin_arg(p.tilesN); pin_arg(p.NE); pin_arg(p.NG);
     if (DUMP) pin_arg(a.acc_dump);
 
@@ -209,7 +209,14 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     // stays scalar
     const int wk = __builtin_amdgcn_readfirstlane(tid / kWaveGroup);
     const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);
-    const int64_t M = a.M, N = a.N;
+    // tokens of this call: M, or (device Params) min(p.m, M) read when the
+    // kernel runs; the grid is sized for M
+    int64_t M = a.M;
+    if (a.params) {
+        const int64_t pm = (int64_t)a.params[kParamM];
+        M = pm < M ? pm : M;
+    }
+    const int64_t N = a.N;
     const int K = (int)a.K;
     const int NG = p.NG, NE = p.NE;
     const int nsteps = K / kBK;
@@ -231,6 +238,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     const int off = lt - grp * GM * p.tilesN;
     const int tile_m = grp * GM + off % gm, tile_n = off / gm;
     const int64_t m0 = (int64_t)tile_m * BM;
+    if (m0 >= M) return;  // a token tile past this step's tokens (uniform: nothing issued yet)
     constexpr int OUTW = MODE == 2 ? BN / 2 : BN;  // output columns per tile
     const int64_t n0 = (int64_t)tile_n * OUTW;
 

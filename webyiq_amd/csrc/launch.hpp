@@ -31,7 +31,13 @@ struct LinearArgs {
     int mode;
     float* y;            // [M, N]; nullable only for the lm_head argmax path
     int32_t* acc_dump;   // nullable: [M, rows, K/Ge] int32 group accumulators
+    // nullable (the GEMM only): device wq_params {pos, seq_len, m, slot}; when
+    // set, M is the capacity and the kernel covers min(m, M) tokens
+    const uint32_t* params;
 };
+// word index of wq_params fields
+constexpr int kParamPos = 0;
+constexpr int kParamM = 2;
 
 struct ArgmaxArgs {
     const uint32_t* ids;  // nullable id map (draft vocabulary)
@@ -73,6 +79,8 @@ struct AttnCombineArgs {
     const float* part;    // [M, H, nch, D + 2]: chunk output sums, chunk max, chunk sum
     int64_t M, H, D, nch;
     int64_t pos;          // position of token 0; token m covers positions 0 ..= pos + m
+                          // (with params: the largest position the call may see)
+    const uint32_t* params;  // nullable: device wq_params, pos read from it at run time
     const float* gate;    // nullable: gate of (m, h, i) at gate[m * gate_stride + h * 2D + D + i]
     int64_t gate_stride;
     int8_t* xq;           // [M, H * D]

@@ -35,6 +35,9 @@ std::string check_size(const std::string& name, const char* what, Buffer b, size
     return {};
 }
 
+// Tokens an op built for `built` tokens runs at step.m (0: as built).
+uint32_t step_tokens(Step st, uint32_t built) { return st.m == 0 || st.m > built ? built : st.m; }
+
 }  // namespace
 
 uint32_t tokens(Path p) {
@@ -90,33 +93,36 @@ Result<OpDef> Builder::gemv(const std::string& name, const std::string& w, uint3
     const Q4 q = wt.value();
     const int32_t g = group_, ga = (int32_t)(a.ga == 0 ? k : a.ga);
     const Acts in = a;
-    return Result<OpDef>::ok(OpDef{name, [=](void* s) {
+    return Result<OpDef>::ok(OpDef{name, [=](void* s, Step) {
         return wq_gemv(s, (const uint32_t*)q.q.ptr, (const uint32_t*)q.s.ptr, n, k, g, (const int8_t*)in.xq.ptr,
                        (const float*)in.dx.ptr, (const int32_t*)in.xs.ptr, t, ga, (int32_t)mode, (float*)y.ptr);
     }});
 }
 
 Result<OpDef> Builder::gemm(const std::string& name, const std::string& w, uint32_t k, uint32_t n, uint32_t mode,
-                            uint32_t m, const Acts& a, Buffer y) {
+                            uint32_t m, const Acts& a, Buffer y, const Buffer* params) {
     std::string e = check_kn(name, k, n, mode);
     if (e.empty() && m == 0) e = fmt("%s: 0 tokens", name.c_str());
     if (e.empty()) e = check_acts(name, k, m, a);
     if (e.empty()) e = check_size(name, "y", y, (size_t)m * n * 4);
+    if (e.empty() && params) e = check_size(name, "params", *params, sizeof(wq_params));
     if (!e.empty()) return Result<OpDef>::err(e);
     auto wt = q4(w, mode == 2 ? 2 * n : n, k);
     if (!wt.is_ok()) return Result<OpDef>::err(wt.error());
     const Q4 q = wt.value();
     const int32_t g = group_, ga = (int32_t)(a.ga == 0 ? k : a.ga);
     const Acts in = a;
-    return Result<OpDef>::ok(OpDef{name, [=](void* s) {
+    const wq_params* pp = params ? (const wq_params*)params->ptr : nullptr;
+    return Result<OpDef>::ok(OpDef{name, [=](void* s, Step st) {
         return wq_gemm(s, (const uint32_t*)q.q.ptr, (const uint32_t*)q.s.ptr, n, k, g, (const int8_t*)in.xq.ptr,
-                       (const float*)in.dx.ptr, (const int32_t*)in.xs.ptr, m, ga, (int32_t)mode, (float*)y.ptr);
+                       (const float*)in.dx.ptr, (const int32_t*)in.xs.ptr, step_tokens(st, m), ga, (int32_t)mode,
+                       (float*)y.ptr, pp);
     }});
 }
 
 Result<OpDef> Builder::matmul(Path path, const std::string& name, const std::string& w, uint32_t k, uint32_t n,
-                              uint32_t mode, const Acts& a, Buffer y, uint32_t m) {
-    if (path == Path::Prefill) return gemm(name, w, k, n, mode, m, a, y);
+                              uint32_t mode, const Acts& a, Buffer y, uint32_t m, const Buffer* params) {
+    if (path == Path::Prefill) return gemm(name, w, k, n, mode, m, a, y, params);
     return gemv(name, w, k, n, mode, tokens(path), a, y);
 }
 
@@ -131,9 +137,9 @@ Result<OpDef> Builder::quant(const std::string& name, uint32_t k, double eps, Bu
     const void* nw = norm ? norm->ptr : nullptr;
     const int32_t g = group_, ga = (int32_t)(a.ga == 0 ? k : a.ga);
     const Acts out = a;
-    return Result<OpDef>::ok(OpDef{name, [=](void* s) {
-        return wq_quant_act(s, (const float*)x.ptr, (const float*)nw, (float)eps, t, k, ga, g, (int8_t*)out.xq.ptr,
-                            (float*)out.dx.ptr, (int32_t*)out.xs.ptr);
+    return Result<OpDef>::ok(OpDef{name, [=](void* s, Step st) {
+        return wq_quant_act(s, (const float*)x.ptr, (const float*)nw, (float)eps, step_tokens(st, t), k, ga, g,
+                            (int8_t*)out.xq.ptr, (float*)out.dx.ptr, (int32_t*)out.xs.ptr);
     }});
 }
 
@@ -155,7 +161,7 @@ Result<OpDef> Builder::quant_gemv(const std::string& name, const std::string& w,
     const void* nw = norm ? norm->ptr : nullptr;
     const int32_t g = group_;
     const Acts out = a;
-    return Result<OpDef>::ok(OpDef{name, [=](void* s) {
+    return Result<OpDef>::ok(OpDef{name, [=](void* s, Step) {
         return wq_quant_gemv(s, (const float*)x.ptr, (const float*)nw, (float)eps, (const uint32_t*)q.q.ptr,
                              (const uint32_t*)q.s.ptr, n, k, g, t, (int32_t)mode, (int8_t*)out.xq.ptr,
                              (float*)out.dx.ptr, (int32_t*)out.xs.ptr, (float*)y.ptr);
@@ -185,7 +191,7 @@ Result<std::vector<OpDef>> Builder::head_ops(const std::string& head, uint32_t k
     const Acts in = a;
     std::vector<OpDef> ops;
     ops.push_back(nq.value());
-    ops.push_back(OpDef{name, [=](void* s) {
+    ops.push_back(OpDef{name, [=](void* s, Step) {
         return wq_lm_head_argmax(s, (const uint32_t*)q.q.ptr, (const uint32_t*)q.s.ptr, v, k, g,
                                  (const int8_t*)in.xq.ptr, (const float*)in.dx.ptr, (const int32_t*)in.xs.ptr, t,
                                  ga, (const uint32_t*)idp, (float*)lgp, (uint32_t*)tok.ptr, workspace.ptr,
@@ -205,7 +211,7 @@ Result<OpDef> Builder::embed(const std::string& name, const std::string& table, 
     if (!wt.is_ok()) return Result<OpDef>::err(wt.error());
     const Q4 q = wt.value();
     const int32_t g = group_;
-    return Result<OpDef>::ok(OpDef{name, [=](void* s) {
+    return Result<OpDef>::ok(OpDef{name, [=](void* s, Step) {
         return wq_embed(s, (const uint32_t*)q.q.ptr, (const uint32_t*)q.s.ptr, v, k, g, (const uint32_t*)tok.ptr, t,
                         (float*)x.ptr);
     }});
@@ -224,7 +230,7 @@ Result<OpDef> Builder::gather_rows(const std::string& name, const std::string& t
     if (!wt.is_ok()) return Result<OpDef>::err(wt.error());
     const Q4 q = wt.value();
     const int32_t g = group_;
-    return Result<OpDef>::ok(OpDef{name, [=](void* s) {
+    return Result<OpDef>::ok(OpDef{name, [=](void* s, Step) {
         return wq_gather_rows(s, (const uint32_t*)q.q.ptr, (const uint32_t*)q.s.ptr, v, k, g,
                               (const uint32_t*)ids.ptr, r, (uint32_t*)dq.ptr, (uint32_t*)ds.ptr);
     }});
@@ -232,7 +238,7 @@ Result<OpDef> Builder::gather_rows(const std::string& name, const std::string& t
 
 Result<OpDef> Builder::attn_combine(const std::string& name, Buffer part, uint32_t t, uint32_t h, uint32_t d,
                                     uint32_t nch, int64_t pos, const Buffer* gate, int64_t gate_stride,
-                                    const Acts& a) {
+                                    const Acts& a, const Buffer* params) {
     std::string e;
     if (d != 64 && d != 128 && d != 256) e = fmt("%s: head dim %u (64, 128 or 256)", name.c_str(), d);
     if (e.empty() && (t == 0 || h == 0 || nch == 0)) e = fmt("%s: empty shape", name.c_str());
@@ -245,12 +251,14 @@ Result<OpDef> Builder::attn_combine(const std::string& name, Buffer part, uint32
         else e = check_size(name, "gate", *gate, ((size_t)(t - 1) * gate_stride + 2 * (size_t)h * d) * 4);
     }
     if (e.empty()) e = check_acts(name, h * d, t, a);
+    if (e.empty() && params) e = check_size(name, "params", *params, sizeof(wq_params));
     if (!e.empty()) return Result<OpDef>::err(e);
     const void* gp = gate ? gate->ptr : nullptr;
     const Acts out = a;
-    return Result<OpDef>::ok(OpDef{name, [=](void* s) {
-        return wq_attn_combine(s, (const float*)part.ptr, t, h, d, nch, pos, (const float*)gp, gate_stride,
-                               (int8_t*)out.xq.ptr, (float*)out.dx.ptr, (int32_t*)out.xs.ptr);
+    const wq_params* pp = params ? (const wq_params*)params->ptr : nullptr;
+    return Result<OpDef>::ok(OpDef{name, [=](void* s, Step st) {
+        return wq_attn_combine(s, (const float*)part.ptr, step_tokens(st, t), h, d, nch, pos, (const float*)gp,
+                               gate_stride, (int8_t*)out.xq.ptr, (float*)out.dx.ptr, (int32_t*)out.xs.ptr, pp);
     }});
 }
 
@@ -267,16 +275,16 @@ Result<OpDef> Builder::mtp_in(const std::string& name, uint32_t k, double eps, B
     if (e.empty()) e = check_acts(name, 2 * k, t, a);
     if (!e.empty()) return Result<OpDef>::err(e);
     const Acts out = a;
-    return Result<OpDef>::ok(OpDef{name, [=](void* s) {
+    return Result<OpDef>::ok(OpDef{name, [=](void* s, Step) {
         return wq_mtp_in(s, (const float*)emb.ptr, (const float*)x.ptr, (const float*)norm_f.ptr,
                          (const float*)norm_e.ptr, (const float*)norm_h.ptr, (float)eps, t, k, (int8_t*)out.xq.ptr,
                          (float*)out.dx.ptr, (int32_t*)out.xs.ptr);
     }});
 }
 
-Result<Unit> encode(const std::vector<OpDef>& ops, void* stream) {
+Result<Unit> encode(const std::vector<OpDef>& ops, void* stream, Step step) {
     for (const OpDef& op : ops) {
-        const int rc = op.launch(stream);
+        const int rc = op.launch(stream, step);
         if (rc != WQ_OK) return Result<Unit>::err(op.name + ": " + wq_last_error());
     }
     return Result<Unit>::ok(Unit{});

@@ -68,10 +68,22 @@ struct Acts {
     uint32_t ga = 0;
 };
 
-// One recorded dispatch (graph.rs:66-71).
+// The step an op list is replayed for (Engine::resolve, lib.rs:207-214):
+// seq_len positions in all, m tokens.  0 means "as built": an op then runs
+// the token count it was built with.  Ops whose token count follows the step
+// (the reference's Dims::Tokens / GemmTiles: quant, gemm, attn_combine) run
+// min(m, built count) tokens; GEMV ops keep their path's count, as the
+// reference's gemv bakes T into the pipeline.
+struct Step {
+    uint32_t seq_len = 0;
+    uint32_t m = 0;
+};
+
+// One recorded dispatch (graph.rs:66-71): the C-ABI call with its arguments
+// bound, resolved against the step when replayed.
 struct OpDef {
     std::string name;
-    std::function<int(void* stream)> launch;  // returns the C ABI's status
+    std::function<int(void* stream, Step step)> launch;  // returns the C ABI's status
 };
 
 class Builder {
@@ -88,13 +100,17 @@ class Builder {
     // 2 silu(gate) * up over the 2n rows of w
     Result<OpDef> gemv(const std::string& name, const std::string& w, uint32_t k, uint32_t n, uint32_t mode,
                        uint32_t t, const Acts& a, Buffer y);
-    // the prefill product over m tokens (graph.rs:200-205)
+    // the prefill product over up to m tokens (graph.rs:200-205); params
+    // (optional): the step's Params buffer (wq_params, 16 bytes of device
+    // memory) the kernel reads when it runs, so the tokens it covers follow
+    // the buffer's m (at most m, the capacity the buffers hold)
     Result<OpDef> gemm(const std::string& name, const std::string& w, uint32_t k, uint32_t n, uint32_t mode,
-                       uint32_t m, const Acts& a, Buffer y);
+                       uint32_t m, const Acts& a, Buffer y, const Buffer* params = nullptr);
     // GEMM for Prefill, GEMV otherwise (graph.rs:207-214); m: the prefill
-    // tokens (the other paths take theirs from the path)
+    // tokens (the other paths take theirs from the path); params as gemm's
     Result<OpDef> matmul(Path path, const std::string& name, const std::string& w, uint32_t k, uint32_t n,
-                         uint32_t mode, const Acts& a, Buffer y, uint32_t m = kPrefillChunk);
+                         uint32_t mode, const Acts& a, Buffer y, uint32_t m = kPrefillChunk,
+                         const Buffer* params = nullptr);
     // int8 quantisation of t rows of x (k wide), optionally RMSNorm'ed with
     // norm (graph.rs:216-222); writes a's three buffers
     Result<OpDef> quant(const std::string& name, uint32_t k, double eps, Buffer x, const Buffer* norm, uint32_t t,
@@ -121,9 +137,12 @@ class Builder {
                               uint32_t r, Buffer ids, Buffer dq, Buffer ds);
     // flash-decoding chunk merge of t tokens x h heads of d dims over nch
     // chunks, positions up to pos + t - 1, optional output gate rows, into
-    // per-32 int8 activations of k = h d (graph.rs:289-291); a.ga must be 32
+    // per-32 int8 activations of k = h d (graph.rs:289-291); a.ga must be 32.
+    // params (optional): the Params buffer; the position is then read from
+    // it when the kernel runs (attn_combine.wgsl:35) and pos is its bound
     Result<OpDef> attn_combine(const std::string& name, Buffer part, uint32_t t, uint32_t h, uint32_t d,
-                               uint32_t nch, int64_t pos, const Buffer* gate, int64_t gate_stride, const Acts& a);
+                               uint32_t nch, int64_t pos, const Buffer* gate, int64_t gate_stride, const Acts& a,
+                               const Buffer* params = nullptr);
     // MTP input stage: per-32 int8 activations [t, 2k] of the normed
     // embedding and hidden state (graph.rs:500-504); a.ga must be 32
     Result<OpDef> mtp_in(const std::string& name, uint32_t k, double eps, Buffer emb, Buffer x, Buffer norm_f,
@@ -140,8 +159,9 @@ class Builder {
     int32_t group_;
 };
 
-// Engine::encode (lib.rs:222-228): launch the ops in order on stream; the
-// first failing op ends the replay with "{op}: {message}".
-Result<Unit> encode(const std::vector<OpDef>& ops, void* stream);
+// Engine::encode (lib.rs:222-228) over Engine::resolve (lib.rs:207-214):
+// launch the ops in order on stream for `step`; the first failing op ends
+// the replay with "{op}: {message}".
+Result<Unit> encode(const std::vector<OpDef>& ops, void* stream, Step step = Step{});
 
 }  // namespace webyiq

@@ -13,7 +13,12 @@ token.  With fused=True each quant -> matmul pair is one wq_quant_gemv call
 (one launch for M <= 2); fused=False issues the quantiser and the GEMV
 separately (bit-identical results).  All buffers are allocated up front;
 `run()` only launches, on one stream, so the sequence can be captured into a
-HIP graph and replayed.
+HIP graph and replayed.  With params (ops.make_params: the step's device
+Params, the reference's uniform of graph.rs:413-416) the chunk merge reads
+its position from that buffer when it runs (attn_combine.wgsl:35), so one
+captured layer serves every position: only the buffer is rewritten between
+replays (lib.rs:312-314, or the GPU itself on the speculative path,
+lib.rs:325).
 """
 import contextlib
 
@@ -24,16 +29,20 @@ from . import ops
 
 class DecodeLayer:
     def __init__(self, w, M, hidden=2048, q_dim=2048, kv_dim=512, ffn=6144, G=128, eps=1e-6,
-                 fused=True, x=None, device="cuda", attention="copy", head_dim=128, pos=511, max_ctx=4096):
+                 fused=True, x=None, device="cuda", attention="copy", head_dim=128, pos=511, max_ctx=4096,
+                 params=None):
         """w: ops.Weights with 'qkv' (q_dim + 2 kv_dim rows), 'o', 'gate_up'
         (2 ffn rows) and 'down' Q4Tensors, plus float tensors 'attn_norm' and
         'mlp_norm'.  x: the residual stream f32 [M, hidden] to update in place
         (layers of one model share it); allocated when None.  attention:
         "copy" or "combine" (chunk partials of tokens at positions pos ..
-        pos + M - 1 in a max_ctx context, head_dim per head)."""
+        pos + M - 1 in a max_ctx context, head_dim per head).  params: the
+        device step parameters; the merge then takes pos from them at run
+        time (any position up to max_ctx - M) and `pos` is unused."""
         assert attention in ("copy", "combine")
         self.w, self.M, self.eps, self.fused, self.attention = w, M, eps, fused, attention
-        self.q_dim, self.pos = q_dim, pos
+        self.q_dim, self.pos, self.params = q_dim, pos, params
+        self.pos_bound = max_ctx - M  # the largest first position the context holds
         f32 = dict(dtype=torch.float32, device=device)
         self.x = torch.zeros((M, hidden), **f32) if x is None else x  # residual stream (in/out)
         self.qkv = torch.empty((M, q_dim + 2 * kv_dim), **f32)
@@ -62,7 +71,10 @@ class DecodeLayer:
         w = self.w
         self._linear("qkv", self.x, self.a_in, norm=w["attn_norm"], y=self.qkv, stream=stream)
         if self.attention == "combine":
-            ops.attn_combine(self.part, self.pos, out=self.a_att, stream=stream)
+            if self.params is not None:
+                ops.attn_combine(self.part, self.pos_bound, out=self.a_att, stream=stream, params=self.params)
+            else:
+                ops.attn_combine(self.part, self.pos, out=self.a_att, stream=stream)
             ops.gemv(w.w("o"), self.a_att, mode=ops.MODE_ACCUMULATE, y=self.x, stream=stream)
         else:
             with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():

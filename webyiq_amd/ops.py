@@ -193,9 +193,33 @@ def _check_linear(w: Q4Tensor, a: Acts):
         raise ValueError(f"acts on {a.xq.device}, the weight on {w.q.device}")
 
 
-def _linear(fn, w: Q4Tensor, a: Acts, mode, y, stream, acc=None):
+def make_params(pos=0, seq_len=0, m=0, slot=0, device="cuda"):
+    """The step parameters as a device tensor u32[4] {pos, seq_len, m, slot}
+    (wq_params; the reference's Params uniform, gemm_q4q8.wgsl:8-13).  Kernels
+    that take it read it when they run, so a recorded call follows its
+    contents; rewrite it with set_params (a copy on the stream)."""
+    return torch.tensor([pos, seq_len, m, slot], dtype=torch.int32, device=device)
+
+
+def set_params(params, pos=0, seq_len=0, m=0, slot=0, stream=None):
+    """Overwrite a make_params tensor in stream order (host -> device copy)."""
+    _check_params(params, params.device)
+    src = torch.tensor([pos, seq_len, m, slot], dtype=torch.int32)
+    with _on(stream):
+        params.copy_(src, non_blocking=False)
+    return params
+
+
+def _check_params(params, device):
+    if params is None:
+        return None
+    return _check(params, "params", _ID_DTYPES, shape=(4,), device=device)
+
+
+def _linear(fn, w: Q4Tensor, a: Acts, mode, y, stream, acc=None, params=None, pass_params=False):
     _check_linear(w, a)
     N = _nrows(w, mode)
+    _check_params(params, a.xq.device)
     with _on(stream):
         y = _out(y, a.M, N, a.xq.device, mode)
         if acc is not None:
@@ -205,6 +229,8 @@ def _linear(fn, w: Q4Tensor, a: Acts, mode, y, stream, acc=None):
                 _ptr(a.xs), a.M, a.GA, mode, _ptr(y)]
         if acc is not None:
             args.append(_ptr(acc))
+        if pass_params:
+            args.append(_ptr(params))
         _lib.call(fn, *args)
     return y
 
@@ -241,20 +267,23 @@ def quant_gemv(w: Q4Tensor, x, norm=None, eps=1e-6, mode=MODE_STORE, y=None, out
     return y, a
 
 
-def gemm(w: Q4Tensor, a: Acts, mode=MODE_STORE, y=None, stream=None):
-    """Prefill GEMM on int8 MFMA (Builder::gemm, gemm_q4q8.wgsl)."""
-    return _linear("wq_gemm", w, a, mode, y, stream)
+def gemm(w: Q4Tensor, a: Acts, mode=MODE_STORE, y=None, stream=None, params=None):
+    """Prefill GEMM on int8 MFMA (Builder::gemm, gemm_q4q8.wgsl).  params
+    (make_params, optional): a.M is then the capacity and the kernel covers
+    the params' m tokens, read when it runs; rows past them are not written."""
+    return _linear("wq_gemm", w, a, mode, y, stream, params=params, pass_params=True)
 
 
-def matmul(path, w: Q4Tensor, a: Acts, mode=MODE_STORE, y=None, stream=None):
-    """Builder::matmul: GEMM for the prefill path, GEMV otherwise."""
+def matmul(path, w: Q4Tensor, a: Acts, mode=MODE_STORE, y=None, stream=None, params=None):
+    """Builder::matmul: GEMM for the prefill path (with params), GEMV otherwise."""
     _check_linear(w, a)
     N = _nrows(w, mode)
+    _check_params(params, a.xq.device)
     with _on(stream):
         y = _out(y, a.M, N, a.xq.device, mode)
         _cuda(w.q, "w.q")
         _lib.call("wq_matmul", _cur(), int(path), _ptr(w.q), _ptr(w.s), N, w.K, w.G,
-                  _ptr(a.xq), _ptr(a.dx), _ptr(a.xs), a.M, a.GA, mode, _ptr(y))
+                  _ptr(a.xq), _ptr(a.dx), _ptr(a.xs), a.M, a.GA, mode, _ptr(y), _ptr(params))
     return y
 
 
@@ -373,10 +402,13 @@ def mtp_in(emb, x, norm_f, norm_e, norm_h, eps=1e-6, out: Optional[Acts] = None,
     return a
 
 
-def attn_combine(part, pos, gate=None, gate_stride=0, G=128, out: Optional[Acts] = None, stream=None) -> Acts:
+def attn_combine(part, pos, gate=None, gate_stride=0, G=128, out: Optional[Acts] = None, stream=None,
+                 params=None) -> Acts:
     """Merge flash-decoding partials part f32 [M, H, nch, D + 2] into the o
     projection's int8 input (attn_combine.wgsl), per-32 scales; optional
-    Qwen3.5 gate rows (gate of head h at h*2D + D of a token's row)."""
+    Qwen3.5 gate rows (gate of head h at h*2D + D of a token's row).  params
+    (make_params, optional): the position is read from it when the kernel
+    runs, and `pos` is the largest it may be (larger values are clamped)."""
     _check(part, "part", torch.float32)
     if part.dim() != 4:
         raise ValueError(f"part: expected [M, H, nch, D + 2], got shape {tuple(part.shape)}")
@@ -384,6 +416,7 @@ def attn_combine(part, pos, gate=None, gate_stride=0, G=128, out: Optional[Acts]
     D = D2 - 2
     if gate is not None:
         _check(gate, "gate", torch.float32, min_numel=(M - 1) * gate_stride + 2 * H * D, device=part.device)
+    _check_params(params, part.device)
     with _on(stream):
         a = out if out is not None else empty_acts(M, H * D, GA=32, G=G, device=part.device)
         a.check("out")
@@ -391,7 +424,7 @@ def attn_combine(part, pos, gate=None, gate_stride=0, G=128, out: Optional[Acts]
             raise ValueError(f"out: attn_combine writes [M, H*D] = {(M, H * D)} activations at GA = 32")
         _cuda(part, "part")
         _lib.call("wq_attn_combine", _cur(), _ptr(part), M, H, D, nch, int(pos), _ptr(gate),
-                  int(gate_stride), _ptr(a.xq), _ptr(a.dx), _ptr(a.xs))
+                  int(gate_stride), _ptr(a.xq), _ptr(a.dx), _ptr(a.xs), _ptr(params))
     return a
 
 
