@@ -7,12 +7,12 @@ One step = one decode GEMV launch (M=1, K=2048, N=6144, int4 group-128 weights,
 per-token int8 activations) on inputs already resident in HBM.  W warm-up
 launches, then exactly K timed launches; launch i uses weight copy i mod R
 (default R = 64 x 6.7 MB = 430 MB > the 256 MB MALL), so every launch streams
-its weights from HBM.  The W and the K launches are captured as two HIP
-graphs (or, with --launch eager, issued directly) and queued on one stream
-behind a gate of read-only passes over a 512 MiB buffer, so the GPU runs
-them back to back with no host submission gap (class Gate); HIP events on
-that stream around the K launches time the region, which is synchronised on
-both sides.
+its weights from HBM.  The W and the K launches are issued one by one (or,
+with --launch graph, captured as two HIP graphs) on one stream behind a gate
+of --settle untimed launches of the same GEMV replayed as a graph, so the
+GPU runs them back to back with no host submission gap and at the clocks of
+back-to-back decode launches (class Gate); HIP events on that stream around
+the K launches time the region, which is synchronised on both sides.
 
 Printed JSON line:
   value       whole-job GEMV throughput, algorithmic GB/s over the K steps
@@ -71,9 +71,14 @@ def parse():
                     help="weight/output copies the prefill GEMMs rotate over (16 = 504 MB, twice the MALL)")
     ap.add_argument("--gemm-warmup", type=int, default=400,
                     help="graph replays before the prefill GEMMs are timed (clocks settle within ~80 ms)")
-    ap.add_argument("--launch", choices=("graph", "eager"), default="graph",
-                    help="timed launches as one captured HIP graph (default) or as eager launches "
-                         "(both queued behind the gate kernel)")
+    ap.add_argument("--launch", choices=("graph", "eager"), default="eager",
+                    help="timed launches issued one by one (default) or as one captured HIP graph, "
+                         "both queued behind the gate (a graph launch adds ~8 us to the timed region)")
+    ap.add_argument("--settle", type=int, default=1000,
+                    help="untimed GEMV launches (other weight copies), replayed as a graph ahead of "
+                         "the warm-up: the gate that covers the host's enqueue and settles the clocks")
+    ap.add_argument("--no-kernel-clock", action="store_true",
+                    help="skip the device-clock duration of single launches (roofline.kernel_us)")
     ap.add_argument("--timeline", action="store_true",
                     help="also replay the GEMV from the timing build (libwebyiq_q4q8_timeline.so) and "
                          "report its per-workgroup phase stamps")
@@ -81,6 +86,11 @@ def parse():
                     help="after the timed region, copy a buffer of this many MiB 8 times "
                          "(the known-size kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
+
+
+def log(msg):
+    """Progress on stderr (the JSON line is the only stdout output)."""
+    print(f"bench.py: {msg}", file=sys.stderr, flush=True)
 
 
 class Launcher:
@@ -125,21 +135,28 @@ def graph_time(torch, launches, reps):
 
 
 class Gate:
-    """Host-independent timing of a launch sequence.  On one stream: a gate
-    of read-only passes over a 512 MiB buffer (sums; ~0.1 ms each), then the
-    warm-up launches, e0, the timed launches, e1.  The gate lasts until the
-    host has enqueued everything behind it (checked: its end event must
-    still be pending when the host is done, else the gate is doubled and the
-    run repeated), so the GPU runs the launches back to back with no host
-    submission gap, and the timed ones start in the steady state the warm-up
-    reached.  The gate leaves no weight copy in the 256 MB MALL and, being
-    read-only, no dirty lines whose write-back the timed launches would pay.
-    Synchronised on both sides."""
+    """Host-independent timing of a launch sequence.  On one stream: a gate,
+    then the warm-up launches, e0, the timed launches, e1.  The gate is either
+    `settle`, untimed launches of the same kernel captured as one HIP graph
+    and replayed, or (without them) read-only passes over a 512 MiB buffer;
+    it lasts until the host has enqueued everything behind it (checked: its
+    end event must still be pending when the host is done, else the gate is
+    doubled and the run repeated), so the GPU runs the launches back to back
+    with no host submission gap.  A settle gate also brings the GPU to the
+    clocks of back-to-back launches: after other work the first ~200-1000
+    launches of the headline GEMV run slower (measured: 20 timed launches
+    averaged 3.84 us after a memory-bound gate, 3.57 us after 1000 settle
+    launches, against 3.50 us over 2000).  Synchronised on both sides."""
 
-    def __init__(self, torch):
+    def __init__(self, torch, settle=()):
         self.torch = torch
-        self.flush = torch.ones(128 << 20, dtype=torch.float32, device="cuda")
-        self.passes = 8
+        self.passes = 1
+        self.settle = list(settle)
+        self.gs = None
+        self.flush = None
+        if not self.settle:
+            self.flush = torch.ones(128 << 20, dtype=torch.float32, device="cuda")
+            self.passes = 8
 
     def _graph(self, seq, s):
         torch = self.torch
@@ -157,11 +174,13 @@ class Gate:
 
     def time(self, seq, graph=True, warm=()):
         """Seconds per launch of `seq` (callables taking a stream), after the
-        `warm` launches on the same stream."""
+        gate and the `warm` launches on the same stream."""
         torch = self.torch
         warm = list(warm)
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
+        if self.settle and self.gs is None:
+            self.gs = self._graph(self.settle, s)
         gw = self._graph(warm, s) if graph else None
         gt = self._graph(seq, s) if graph else None
         for _ in range(6):
@@ -170,7 +189,10 @@ class Gate:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             with torch.cuda.stream(s):
                 for _ in range(self.passes):
-                    self.flush.sum()
+                    if self.gs is not None:
+                        self.gs.replay()
+                    else:
+                        self.flush.sum()
                 eg.record(s)
                 cs = ctypes.c_void_p(s.cuda_stream)
                 if gw is not None:
@@ -242,7 +264,9 @@ def main():
     # launches on copies W, W+1, ... (mod R): a copy comes back only after R
     # launches (430 MB), so every timed launch streams its weights from HBM
     steps, warmup = max(1, args.steps), max(0, args.warmup)
-    gate = Gate(torch)
+    # the gate: settle launches on the copies after the timed ones, replayed
+    # as a graph while the host enqueues the warm-up and timed launches
+    gate = Gate(torch, [launches[(warmup + steps + j) % R] for j in range(args.settle)])
     graph = args.launch == "graph"
     t_launch = gate.time([launches[(warmup + i) % R] for i in range(steps)], graph=graph,
                          warm=[launches[i % R] for i in range(warmup)])
@@ -277,11 +301,14 @@ def main():
         "gemv_us_per_launch": round(t_launch * 1e6, 3),
         "launch": args.launch,
         "gate_covered_host_enqueue": gate_covered,
+        "settle_launches": args.settle * gate.passes,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "parity": {"gemv_vs_oracle_bit_exact": parity},
     }
-    kc = kernel_clock(torch, gate, [ln.args for ln in launches])
+    log(f"headline: {steps} timed launches, {t_launch * 1e6:.3f} us per launch")
+    kc = None if args.no_kernel_clock else kernel_clock(
+        torch, Gate(torch, [launches[j % R] for j in range(256)]), [ln.args for ln in launches])
     if kc is not None:
         # the device-clock duration of one launch (first workgroup entry to
         # last store, the timing build), beside the per-launch figure above
@@ -303,6 +330,7 @@ def main():
         del src, dst
 
     if not args.no_gemm:
+        log("prefill GEMMs")
         detail = bench_gemm(torch, lib, ops, orc, ref, args)
         # flat scalars per shape (us, TOP/s, fraction of the int8 peak); the
         # per-shape roofline blocks and parity figures under prefill_detail
@@ -311,9 +339,11 @@ def main():
         out["prefill_detail"] = detail
 
     if not args.no_configs:
+        log("configs")
         out["configs"] = bench_configs(torch, lib, ops, orc)
 
     if not args.no_cpu:
+        log("cpu baseline")
         out["cpu_baseline"] = cpu_baseline(torch, ref, wq, ws, K, G, x, nbytes, args.cpu_seconds)
 
     print(json.dumps(out), flush=True)
@@ -344,9 +374,9 @@ def read_stamps(T):
 
 def kernel_clock(torch, gate, launch_args, n=32):
     """Device-clock duration of single headline launches: n launches of the
-    timing build, each on a different weight copy after the MALL flush, each
-    from the first workgroup's entry stamp to the last workgroup's
-    after-store stamp (us; median and range)."""
+    timing build, each on a different weight copy after the gate, each from
+    the first workgroup's entry stamp to the last workgroup's after-store
+    stamp (us; median and range)."""
     T = timeline_lib()
     if T is None:
         return None
@@ -359,7 +389,7 @@ def kernel_clock(torch, gate, launch_args, n=32):
     return {"median_us": round(float(np.median(durs)), 3), "min_us": round(float(np.min(durs)), 3),
             "max_us": round(float(np.max(durs)), 3), "launches": n,
             "how": "timing build, s_memrealtime (100 MHz): first workgroup entry to last workgroup's "
-                   "after-store stamp, single cold launches"}
+                   "after-store stamp, single launches each after the settle gate"}
 
 
 def bench_timeline(torch, launch_args):
