@@ -446,8 +446,12 @@ def bench_gemm(torch, lib, ops, orc, ref, args):
         s = [torch.from_numpy(ws.view(np.int32)).cuda() for _ in range(copies)]
         a = ops.quant(torch.from_numpy(x).cuda(), G=128)
         ys = [torch.empty((M, N), dtype=torch.float32, device="cuda") for _ in range(copies)]
+        # the split-K workspace (one byte when the shape is not split), shared
+        # by the launches, which are stream-ordered
+        wsp = ops.gemm_workspace(N, K, 128, M)
+        split = wsp.numel() > 1
         # parity on 16 sampled tokens against the oracle (rel 1e-5, max-norm)
-        ops.gemm(ops.Q4Tensor(q[0], s[0], K, 128), a, y=ys[0])
+        ops.gemm(ops.Q4Tensor(q[0], s[0], K, 128), a, y=ys[0], workspace=wsp)
         idx = np.linspace(0, M - 1, 16).astype(int)
         xq, dx, xs = orc.quant_act(x[idx], None, 128)
         want = orc.linear(wq, ws, K, 128, xq, dx, xs)
@@ -459,7 +463,8 @@ def bench_gemm(torch, lib, ops, orc, ref, args):
             sys.exit(1)
         launches = [Launcher(lib, "wq_gemm", [P(q[i].data_ptr()), P(s[i].data_ptr()), N, K, 128,
                                               P(a.xq.data_ptr()), P(a.dx.data_ptr()), P(a.xs.data_ptr()),
-                                              M, K, 0, P(ys[i].data_ptr()), None]) for i in range(copies)]
+                                              M, K, 0, P(ys[i].data_ptr()), None, P(wsp.data_ptr()),
+                                              wsp.numel()]) for i in range(copies)]
         # warm-up long enough for the clocks to settle (the first ~30-80 ms
         # of MFMA load run measurably slower), then the median of three timings
         graph_time(torch, launches, max(1, args.gemm_warmup))
@@ -472,6 +477,7 @@ def bench_gemm(torch, lib, ops, orc, ref, args):
             "roofline": {"bound": "mfma", "achieved": round(ops_ / t / 1e12, 1), "peak": INT8_PEAK_TOPS,
                          "unit": "TOP/s", "frac": round(ops_ / t / 1e12 / INT8_PEAK_TOPS, 4)},
             "parity_vs_oracle_rel": rel,
+            "k_split_pairs": split,
         }
         del q, s, ys
         torch.cuda.empty_cache()
@@ -737,7 +743,7 @@ def bench_configs(torch, lib, ops, orc):
     ys = [torch.empty((M, N), dtype=torch.float32, device="cuda") for _ in range(8)]
     launches = [Launcher(lib, "wq_gemm", [P(q.data_ptr()), P(sc.data_ptr()), N, K, 32, P(a.xq.data_ptr()),
                                           P(a.dx.data_ptr()), P(a.xs.data_ptr()), M, K, 0, P(ys[i].data_ptr()),
-                                          None])
+                                          None, None, 0])
                 for i, (q, sc) in enumerate(ws)]
     graph_time(torch, launches, 50)
     t = graph_time(torch, launches, 10)

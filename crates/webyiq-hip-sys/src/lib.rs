@@ -61,7 +61,8 @@ extern "C" {
                          xs: *mut i32, y: *mut f32) -> i32;
     pub fn wq_gemm(stream: *mut c_void, wq: *const u32, ws: *const u32, n: i64, k: i64, g: i32, xq: *const i8,
                    dx: *const f32, xs: *const i32, m: i64, ga: i32, mode: i32, y: *mut f32,
-                   params: *const WqParams) -> i32;
+                   params: *const WqParams, workspace: *mut c_void, workspace_bytes: usize) -> i32;
+    pub fn wq_gemm_workspace_bytes(n: i64, k: i64, g: i32, m: i64, ga: i32, mode: i32) -> usize;
     pub fn wq_matmul(stream: *mut c_void, path: i32, wq: *const u32, ws: *const u32, n: i64, k: i64, g: i32,
                      xq: *const i8, dx: *const f32, xs: *const i32, m: i64, ga: i32, mode: i32,
                      y: *mut f32, params: *const WqParams) -> i32;
@@ -154,13 +155,17 @@ pub unsafe fn gemv(st: Stream, w: &Q4Weight, n: i64, a: &Acts, mode: i32, y: *mu
 
 /// `Builder::gemm`: prefill GEMM on int8 MFMA, any token count.  With a
 /// non-null `params` (the engine's params buffer), `a.m` is the capacity and
-/// the kernel covers `params.m` tokens, read when it runs.
+/// the kernel covers `params.m` tokens, read when it runs.  `workspace`
+/// (null, or `wq_gemm_workspace_bytes` bytes zeroed once) lets the library
+/// split K between workgroup pairs.
 ///
 /// # Safety
 /// All pointers must be device memory of the documented sizes.
 pub unsafe fn gemm(st: Stream, w: &Q4Weight, n: i64, a: &Acts, mode: i32, y: *mut f32,
-                   params: *const WqParams) -> Result<(), String> {
-    check(wq_gemm(st.0, w.q, w.s, n, w.k, w.g, a.xq, a.dx, a.xs, a.m, a.ga, mode, y, params))
+                   params: *const WqParams, workspace: *mut c_void,
+                   workspace_bytes: usize) -> Result<(), String> {
+    check(wq_gemm(st.0, w.q, w.s, n, w.k, w.g, a.xq, a.dx, a.xs, a.m, a.ga, mode, y, params, workspace,
+                  workspace_bytes))
 }
 
 /// `Builder::matmul`: the engine's `Path` picks the GEMV or the GEMM.

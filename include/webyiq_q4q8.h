@@ -150,10 +150,26 @@ int wq_quant_gemv(void* stream, const float* x, const float* norm_w, float eps,
  * hardware order) and per-32 activations fold one chain per output (the
  * GEMV: chains and a tree): the fp32 outputs agree with wq_gemv within
  * rel 1e-5.
+ * workspace (device, nullable, 256-byte aligned; no counterpart in the
+ * reference): when it holds at least wq_gemm_workspace_bytes(...) > 0 bytes
+ * for the call's shape, the K steps of each output tile may be split between
+ * two workgroups whose partial sums meet in it (the first half's added to
+ * the second's, one fixed order: outputs are deterministic and within
+ * rel 1e-5 of the unsplit launch).  It must be zero before its first use
+ * (wq_workspace_clear) and every call leaves its flags zero again; calls
+ * sharing one workspace must not overlap.  A partner's wait is bounded
+ * (~0.5 s); if it ran out, that tile's outputs are NaN and the workspace is
+ * to be cleared before the next call.  NULL, or fewer bytes: the unsplit
+ * launch.
  */
 int wq_gemm(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K,
             int32_t G, const int8_t* xq, const float* dx, const int32_t* xs,
-            int64_t M, int32_t GA, int32_t mode, float* y, const wq_params* params);
+            int64_t M, int32_t GA, int32_t mode, float* y, const wq_params* params,
+            void* workspace, size_t workspace_bytes);
+
+/* Bytes of workspace wq_gemm can use for this shape (M the capacity); 0
+ * when the shape is never split. */
+size_t wq_gemm_workspace_bytes(int64_t N, int64_t K, int32_t G, int64_t M, int32_t GA, int32_t mode);
 
 /*
  * Builder::matmul (graph.rs:207-214): WQ_PATH_PREFILL -> wq_gemm (with

@@ -68,3 +68,31 @@ def test_library_device_code_has_no_packed_fp32(tmp_path):
         hits = PK.findall(asm)
         assert not hits, f"{o.name}: packed fp32 ops {sorted(set(hits))}"
     assert kernels > 0
+
+
+@pytest.mark.skipif(not (os.path.exists(hipbuild.LIB) and os.path.exists(OBJDUMP)),
+                    reason="library not built or llvm-objdump missing")
+def test_production_gemm_and_headline_gemv_use_no_scratch(tmp_path):
+    """Register spills show up as a private segment: none in the GEMM
+    instances that serve calls (the group-sum dump instances, a test hook,
+    are exempt) nor in the headline decode GEMV."""
+    lib = tmp_path / "lib.so"
+    shutil.copy(hipbuild.LIB, lib)
+    subprocess.run([OBJDUMP, "--offloading", str(lib)], check=True, capture_output=True, cwd=tmp_path)
+    readelf = "/opt/rocm/llvm/bin/llvm-readelf"
+    scratch = {}
+    for o in sorted(p for p in tmp_path.iterdir() if "amdgcn" in p.name and "gfx950" in p.name):
+        notes = subprocess.run([readelf, "--notes", str(o)], check=True, capture_output=True, text=True).stdout
+        name = None
+        for line in notes.splitlines():
+            m = re.match(r"\s+\.name:\s+(\S+)", line)
+            if m:
+                name = m.group(1)
+            m = re.match(r"\s+\.private_segment_fixed_size:\s+(\d+)", line)
+            if m and name:
+                scratch[name] = int(m.group(1))
+    gemm = {k: v for k, v in scratch.items() if "gemm_kernel" in k and k.endswith("ELb0EEEvNS0_10GemmParamsE")}
+    assert len(gemm) >= 30
+    assert not {k: v for k, v in gemm.items() if v}, "spilling GEMM instances"
+    head = [k for k in scratch if "gemv_kernelILi1ELi0ELi128ELb1ELi2ELb0ELb0E" in k]
+    assert head and all(scratch[k] == 0 for k in head)

@@ -21,7 +21,7 @@ def declared_symbols():
 
 def test_exports_every_declared_symbol():
     names = declared_symbols()
-    assert len(names) == 19
+    assert len(names) == 20
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(_lib.PROTOTYPES)
@@ -30,9 +30,9 @@ def test_exports_every_declared_symbol():
 
 
 def gemv(*, wq=A16, ws=A4, N=64, K=2048, G=128, xq=A16, dx=A4, xs=A4, M=1, GA=None, mode=0, y=A4,
-         fn="wq_gemv", params=None):
+         fn="wq_gemv", params=None, workspace=None, wbytes=0):
     GA = K if GA is None else GA
-    extra = [params] if fn == "wq_gemm" else []
+    extra = [params, workspace, wbytes] if fn == "wq_gemm" else []
     return getattr(L, fn)(None, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, *extra)
 
 
@@ -66,6 +66,24 @@ def test_gemv_token_and_k_limits():
     assert gemv(N=1 << 20, K=8192, mode=2, fn="wq_gemm") == _lib.WQ_ESHAPE
     # the step parameters are device words read by the kernel: 4-byte aligned
     assert gemv(params=ctypes.c_void_p(0x10002), fn="wq_gemm") == _lib.WQ_EALIGN and "params" in err()
+    # the split-K workspace is 256-byte aligned
+    assert gemv(workspace=ctypes.c_void_p(0x10040), wbytes=1 << 20, fn="wq_gemm") == _lib.WQ_EALIGN
+    assert "workspace" in err()
+
+
+def test_gemm_workspace_bytes():
+    """The split plan's workspace: zero for shapes that never split (short K,
+    per-32 activations, grids that fill the chip), flags plus 128 x width
+    partial sums per tile otherwise."""
+    wsb = L.wq_gemm_workspace_bytes
+    assert wsb(6144, 2048, 128, 1024, 2048, 0) == 0          # K = 2048: 16 steps
+    assert wsb(2048, 6144, 128, 1024, 32, 0) == 0            # per-32 activations
+    n = wsb(2048, 6144, 128, 1024, 6144, 0)                  # width 128 split in pairs
+    tiles = 8 * 16
+    assert n == ((tiles * 64 + 255) // 256) * 256 + tiles * 128 * 128 * 4
+    m512 = wsb(2048, 6144, 128, 512, 6144, 1)               # width 64 split in pairs
+    assert m512 == ((4 * 32 * 64 + 255) // 256) * 256 + 4 * 32 * 128 * 64 * 4
+    assert wsb(2048, 6144, 64, 1024, 6144, 0) == 0           # unsupported group: no plan
 
 
 def test_matmul_paths():

@@ -354,6 +354,67 @@ def test_gemm_prefill_sizes(M, K, N):
     assert np.all(np.isfinite(got))
 
 
+SPLIT_CASES = [
+    # M, K, N, G, mode: shapes whose plan splits K between workgroup pairs
+    (1024, 6144, 2048, 128, 0),   # width 128, 256 workgroups
+    (512, 6144, 2048, 128, 1),    # width 64, += residual
+    (256, 6144, 2048, 128, 0),
+    (512, 4096, 1024, 128, 2),    # gate/up pairs (width 128)
+    (384, 4096, 2048, 32, 0),     # per-token group 32
+    (200, 8192, 640, 128, 1),     # ragged token and row tiles, 32 steps per half
+]
+
+
+@pytest.mark.parametrize("M,K,N,G,mode", SPLIT_CASES)
+def test_gemm_split_k(M, K, N, G, mode):
+    """K split between workgroup pairs (wq_gemm with a workspace): against the
+    oracle within rel 1e-5 on every row of the first and last tile and one of
+    every 8 elsewhere; within rel 1e-5 of the unsplit launch; bit-identical
+    over repeated calls (the two partials are added in one fixed order); the
+    workspace's flags zero again after every call; and with device Params at
+    m below the capacity, the rows past m untouched."""
+    note(f"gemm split-K M={M} K={K} N={N} G={G} mode={mode}")
+    rows = 2 * N if mode == 2 else N
+    wq, ws, x, xq, dx, xs = setup_linear(M + K + N + mode, M, K, rows, G, None)
+    y0 = np.random.default_rng(4).normal(size=(M, N)).astype(np.float32) if mode == 1 else None
+    w = ops.Q4Tensor.from_numpy(wq, ws, K, G)
+    a = dev_acts(xq, dx, xs, K, G)
+    nws = ops._lib.load().wq_gemm_workspace_bytes(N, K, G, M, K, mode)
+    assert nws > 0, "this shape should split"
+    wsp = ops.gemm_workspace(N, K, G, M, mode=mode)
+    runs = [host(ops.gemm(w, a, mode=mode, y=dev(y0) if mode == 1 else None, workspace=wsp)) for _ in range(3)]
+    for r in runs[1:]:
+        assert np.array_equal(r.view(np.uint32), runs[0].view(np.uint32))
+    # the plan's tile count from the workspace size (flag lines, then 128 x
+    # width partial sums per tile)
+    plans = [(bn, ((M + 127) // 128) * -(-N // (bn // 2 if mode == 2 else bn))) for bn in (64, 128)]
+    T = [t for bn, t in plans if -(-64 * t // 256) * 256 + t * 128 * bn * 4 == nws]
+    assert len(T) == 1, (nws, plans)
+    T = T[0]
+
+    def flags_clear():
+        return not host(wsp[: 64 * T]).view(np.uint32)[::16].any()
+    assert flags_clear(), "flags left set"
+    got = runs[0]
+    unsplit = host(ops.gemm(w, a, mode=mode, y=dev(y0) if mode == 1 else None))
+    assert rel_err(got, unsplit) < 1e-5
+    idx = np.unique(np.concatenate([np.arange(0, min(128, M)), np.arange(max(0, M - 128), M),
+                                    np.arange(0, M, 8) + (np.arange(0, M, 8) // 128) % 8]))
+    idx = idx[idx < M]
+    want = oracle_linear_tokens(wq, ws, K, G, xq[idx], dx[idx], xs[idx], mode=mode,
+                                y=y0[idx] if mode == 1 else None)
+    assert rel_err(got[idx], want) < 1e-5
+    # device Params below the capacity: the pairs of tiles past m both end
+    m = M // 2 + 3
+    base = y0 if mode == 1 else np.full((M, N), np.nan, np.float32)
+    y = dev(base)
+    ops.gemm(w, a, mode=mode, y=y, workspace=wsp, params=ops.make_params(m=m))
+    gp = host(y)
+    assert np.array_equal(gp[:m].view(np.uint32), got[:m].view(np.uint32))
+    assert np.array_equal(gp[m:].view(np.uint32), base[m:].view(np.uint32))
+    assert flags_clear()
+
+
 @pytest.mark.parametrize("M,mode,stride", [(2048, 0, 8), (4096, 2, 32)])
 def test_gemm_group32_wide_widths(M, mode, stride):
     """Per-token activations at group 32 on the widths the launcher picks for

@@ -72,7 +72,7 @@ def test_crate_files_exist():
 def test_every_header_function_bound_with_the_same_signature():
     c = c_declarations()
     r = rust_declarations()
-    assert len(c) == 19
+    assert len(c) == 20
     assert set(c) == set(r), (set(c) ^ set(r))
     for name, (cret, cargs) in c.items():
         rret, rargs = r[name]

@@ -34,7 +34,8 @@ PROTOTYPES = {
     "wq_quant_act": ([_P, _P, _P, _F, _I64, _I64, _I32, _I32, _P, _P, _P], ctypes.c_int),
     "wq_gemv": (_LINEAR, ctypes.c_int),
     "wq_quant_gemv": ([_P, _P, _P, _F, _P, _P, _I64, _I64, _I32, _I64, _I32, _P, _P, _P, _P], ctypes.c_int),
-    "wq_gemm": (_LINEAR + [_P], ctypes.c_int),
+    "wq_gemm": (_LINEAR + [_P, _P, _SZ], ctypes.c_int),
+    "wq_gemm_workspace_bytes": ([_I64, _I64, _I32, _I64, _I32, _I32], _SZ),
     "wq_gemv_debug_acc": (_LINEAR + [_P], ctypes.c_int),
     "wq_gemm_debug_acc": (_LINEAR + [_P], ctypes.c_int),
     "wq_matmul": ([_P, _I32] + _LINEAR[1:] + [_P], ctypes.c_int),

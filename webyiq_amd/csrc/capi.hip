@@ -172,7 +172,7 @@ int gemv_impl(const char* fn, void* stream, const uint32_t* wq, const uint32_t* 
 int gemm_impl(const char* fn, void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N,
               int64_t K, int32_t G, const int8_t* xq, const float* dx, const int32_t* xs,
               int64_t M, int32_t GA, int32_t mode, float* y, int32_t* acc,
-              const wq_params* params = nullptr) {
+              const wq_params* params = nullptr, void* workspace = nullptr, size_t workspace_bytes = 0) {
     int rc = check_linear(fn, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, true);
     if (rc) return rc;
     // the GEMM stages tiles with 32-bit byte offsets from each operand's base
@@ -182,7 +182,10 @@ int gemm_impl(const char* fn, void* stream, const uint32_t* wq, const uint32_t* 
         return fail(WQ_ESHAPE, "%s: M = %lld, rows = %lld, K = %lld address more than 4 GiB of one operand; "
                     "split the call along M or N", fn, (long long)M, (long long)rows, (long long)K);
     if (params) REQUIRE_ALIGN(params, 4);
+    if (workspace) REQUIRE_ALIGN(workspace, 256);
     auto a = make_args(wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, acc, params);
+    a.workspace = workspace;
+    a.workspace_bytes = workspace ? workspace_bytes : 0;
     return hip_status(wq::launch_gemm(a, static_cast<hipStream_t>(stream)), fn);
 }
 
@@ -248,8 +251,21 @@ int wq_quant_gemv(void* stream, const float* x, const float* norm_w, float eps, 
 
 int wq_gemm(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K, int32_t G,
             const int8_t* xq, const float* dx, const int32_t* xs, int64_t M, int32_t GA,
-            int32_t mode, float* y, const wq_params* params) {
-    return gemm_impl("wq_gemm", stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, nullptr, params);
+            int32_t mode, float* y, const wq_params* params, void* workspace, size_t workspace_bytes) {
+    return gemm_impl("wq_gemm", stream, wq, ws, N, K, G, xq, dx, xs, M, GA, mode, y, nullptr, params, workspace,
+                     workspace_bytes);
+}
+
+size_t wq_gemm_workspace_bytes(int64_t N, int64_t K, int32_t G, int64_t M, int32_t GA, int32_t mode) {
+    if (N < 1 || M < 1 || K < 128 || K % 128 != 0 || (G != 32 && G != 128) || mode < 0 || mode > 2) return 0;
+    wq::LinearArgs a{};
+    a.N = N;
+    a.K = K;
+    a.G = G;
+    a.M = M;
+    a.GA = GA;
+    a.mode = mode;
+    return wq::gemm_workspace_bytes(a);
 }
 
 int wq_gemv_debug_acc(void* stream, const uint32_t* wq, const uint32_t* ws, int64_t N, int64_t K,

@@ -48,10 +48,23 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
+// Spin limit of a split-K partner's wait for the first half's partial sums
+// (each poll one device-coherent load plus a short sleep; ~0.5 s, far beyond
+// any launch).
+constexpr unsigned kSplitSpinLimit = 1u << 22;
+// s_getreg operand of HW_REG_XCC_ID (hardware register 20 on gfx940 and
+// later), bits 3:0: the XCD the wave runs on
+constexpr int kHwRegXccId = 20 | (0 << 6) | ((4 - 1) << 11);
+
 struct GemmParams {
     LinearArgs a;
     int tilesM, tilesN;
     int NE, NG;
+    // split K across workgroup pairs (FAST formats): workspace of per-tile
+    // ready flags (one 64-byte line each) and partial sums
+    int split;
+    unsigned int* flags;  // [T] lines
+    float* part;          // [T][128 * BN] partial sums of the first half
 };
 
 // Chunk swizzles: activation rows are 128 bytes (8 chunks), packed weight
@@ -219,11 +232,22 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     const int64_t N = a.N;
     const int K = (int)a.K;
     const int NG = p.NG, NE = p.NE;
-    const int nsteps = K / kBK;
 
     // XCD-aware tile order: consecutive tiles (same weight rows) on one XCD
     const int T = p.tilesM * p.tilesN;
-    const int bid = blockIdx.x;
+    int bid = blockIdx.x;
+    // Split K (FAST formats): workgroups T.. 2T-1 take the second half of the
+    // K steps of tile bid - T; with T a multiple of 8 the pair shares an XCD.
+    // (Widths up to 128 only: the exchange's registers do not fit beside the
+    // wider tiles' accumulators.)
+    constexpr bool SPLITOK = FAST && BN <= 128;
+    const bool split = SPLITOK && p.split;
+    const int half = split && bid >= T ? 1 : 0;
+    bid -= half * T;
+    const int nsteps = split ? K / kBK / 2 : K / kBK;  // this workgroup's K steps
+    const int s_begin = half * nsteps;
+    const int NGL = split ? NG / 2 : NG;               // its weight groups
+    const int g_begin = half * NGL;
     const int xcd = bid % kXcds, li = bid / kXcds;
     const int per = T / kXcds, rem = T % kXcds;
     const int lt = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + li;
@@ -297,7 +321,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     // otherwise fetches BN scattered 4-byte words, one cache-line request
     // each.  Measured: K = 6144, N = 2048 27.08 -> 25.49 us; at K = 2048 (16
     // steps) the preload's start-up cost outweighs it, 22.31 -> 22.65 us.
-    const int NGPs = NG + 1 - (NG & 1);  // odd row stride
+    const int NGPs = NGL + 1 - (NGL & 1);  // odd row stride
     // (the last 64-word instruction may run up to 63 words past BN rows)
     const bool spre = FAST && !G32 && nsteps >= 32 && BN * NGPs + 64 <= BN * SP_NGP;  // uniform
     const uint32_t* sp_lds = reinterpret_cast<const uint32_t*>(lds + SP_BASE);
@@ -308,8 +332,8 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     auto stage_at = [&](int st, int b) -> uint32_t { return lds0 + (uint32_t)(st * ST_SZ + b); };
     auto dma = [&](int step, const int st) {
         step = step < nsteps ? step : nsteps - 1;
-        const int8_t* xq = a.xq + step * kBK;
-        const uint32_t* ws = a.ws + step * NGS;
+        const int8_t* xq = a.xq + (s_begin + step) * kBK;
+        const uint32_t* ws = a.ws + (s_begin + step) * NGS;
 #pragma unroll
         for (int i = 0; i < A_PW; ++i) dma16_at(xq, a_off[i], stage_at(st, 1024 * (A_PW * wave + i)));
         if constexpr (PAIRB) {
@@ -319,7 +343,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
             // passed): the half of a lane's chunk is bit 2 of
             // (lane % 8) ^ swz_p(r), = ((lane >> 2) ^ block) & 1
             const int s0 = step & ~1;
-            const uint8_t* wq = reinterpret_cast<const uint8_t*>(a.wq) + s0 * (kBK / 2);
+            const uint8_t* wq = reinterpret_cast<const uint8_t*>(a.wq) + (s_begin + s0) * (kBK / 2);
             const bool tail = s0 + 1 >= nsteps;  // uniform
 #pragma unroll
             for (int i = 0; i < B_PW; ++i) {
@@ -328,7 +352,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
                 dma16_at(wq, off, lds0 + (uint32_t)(PB_BASE + (st >> 1) * 2 * B_SZ + 1024 * blk));
             }
         } else {
-            const uint8_t* wq = reinterpret_cast<const uint8_t*>(a.wq) + step * (kBK / 2);
+            const uint8_t* wq = reinterpret_cast<const uint8_t*>(a.wq) + (s_begin + step) * (kBK / 2);
 #pragma unroll
             for (int i = 0; i < B_PW; ++i) dma16_at(wq, b_off[i], stage_at(st, A_SZ + 1024 * (B_PW * wave + i)));
         }
@@ -375,8 +399,9 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     // when it is used.
     constexpr int NSL = TN <= 2 ? 2 : TN == 3 ? 1 : 0;
     constexpr int NSA = NSL > 0 ? NSL : 1;  // register slots
-    const int nfull = NG % 8 == 0 ? NG / 8 : 0;  // full blocks (32-byte aligned rows: K a multiple of 1024)
-    const int nblk = (NG + 7) / 8;
+    // (with split K, this workgroup's groups g_begin .. g_begin + NGL - 1)
+    const int nfull = NGL % 8 == 0 ? NGL / 8 : 0;  // full blocks (32-byte aligned rows: K a multiple of 1024)
+    const int nblk = (NGL + 7) / 8;
     const int32_t* xr[TM];
     const uint32_t* sr[TN];
     int32_t xv[NSA][TM][8];
@@ -403,11 +428,11 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int u = 0; u < 8; ++u) x[i][u] = xr[i][b + u < NG ? b + u : NG - 1];
+            for (int u = 0; u < 8; ++u) x[i][u] = xr[i][b + u < NGL ? b + u : NGL - 1];
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int u = 0; u < 8; ++u) w[j][u] = sr[j][b + u < NG ? b + u : NG - 1];
+            for (int u = 0; u < 8; ++u) w[j][u] = sr[j][b + u < NGL ? b + u : NGL - 1];
     };
     auto mt_load = [&](auto slot, int blk) {
         constexpr int S = decltype(slot)::value;
@@ -418,9 +443,9 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
     using ic1 = std::integral_constant<int, NSA - 1>;
     auto mt_rows = [&]() {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) xr[i] = a.xs + trow(wm * 64 + 32 * i + l32) * NE;
+        for (int i = 0; i < TM; ++i) xr[i] = a.xs + trow(wm * 64 + 32 * i + l32) * NE + g_begin;
 #pragma unroll
-        for (int j = 0; j < TN; ++j) sr[j] = a.ws + wrow(bcol(j)) * NG;
+        for (int j = 0; j < TN; ++j) sr[j] = a.ws + wrow(bcol(j)) * NG + g_begin;
     };
     if constexpr (FAST && NSL >= 1) {
         mt_rows();
@@ -435,7 +460,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
         for (int i = wid; i < nins; i += NWAVES) {
             const int pw = 64 * i + lane;
             const int r = pw / NGPs, gg = pw - r * NGPs;
-            const uint32_t src = r < BN && gg < NG ? (uint32_t)(wrow(r) * NG + gg) : 0u;  // padding: word 0
+            const uint32_t src = r < BN && gg < NGL ? (uint32_t)(wrow(r) * NG + g_begin + gg) : 0u;  // padding: word 0
             dma4_at(a.ws, 4 * src, lds0 + (uint32_t)(SP_BASE + 256 * i));
         }
     }
@@ -469,14 +494,14 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const int32_t v = b + u < NG ? xv[i][u] : 0;
+                const int32_t v = b + u < NGL ? xv[i][u] : 0;
                 xa[i][u] = (_Float16)(h == 0 ? (float)((v >> 6) * 64) : (float)(v & 63));
             }
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int u = 0; u < 8; ++u)
-                mb[j][u] = b + u < NG ? __builtin_bit_cast(_Float16, (unsigned short)(wv[j][u] >> 16))
+                mb[j][u] = b + u < NGL ? __builtin_bit_cast(_Float16, (unsigned short)(wv[j][u] >> 16))
                                       : (_Float16)0.0f;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -521,7 +546,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
 
     const int rows_total = MODE == 2 ? 2 * (int)N : (int)N;
     auto dump = [&](int step, int e_local, int i, int br, const v16i& acc) {
-        const int64_t e = (int64_t)step * NES + e_local;
+        const int64_t e = (int64_t)(s_begin + step) * NES + e_local;
         const int64_t nn = n0 + (MODE == 2 ? (br < BN / 2 ? br : br - BN / 2) : br);
         const int64_t wr = MODE == 2 && br >= BN / 2 ? nn + N : nn;
 #pragma unroll
@@ -772,6 +797,116 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
         ihi = wk + 1;
     }
 
+    // Split K: the first half's workgroup hands its partial sums (this
+    // thread's subtile row ilo, every column) to its partner through the
+    // workspace and ends; the partner adds them to its own, first half
+    // first (one fixed order), and runs the epilogue.  The partial stores
+    // and loads are agent-scope atomics (sc1: performed at the device's
+    // coherence point, past a non-coherent L2), so the same argument as the
+    // lm_head argmax combine orders them without a release fence: the
+    // stores are complete (vmcnt 0) in every wave before the barrier, the
+    // flag is set after it, and the partner's loads are issued after its
+    // poll has seen the flag.  The partner waits only for a workgroup of
+    // lower index (dispatched before it, waiting for nothing), and the wait
+    // is bounded: if it ran out, the tile's outputs are written as NaN.
+    if constexpr (SPLITOK) {
+        if (split) {
+            // this thread's values, subtile row wk, as 4 x TN 16-byte chunks
+            // (compile-time indices only: a run-time index would put facc in
+            // scratch memory); chunk c of this thread at slot[c * 64]
+            static_assert(TN <= 2, "the exchange holds 8 chunks in flight");
+            v4f* slot = reinterpret_cast<v4f*>(p.part) + (size_t)lt * (BM * BN / 4) +
+                        (size_t)(tid >> 6) * (TN * 4 * 64) + lane;
+            unsigned int* flag = p.flags + (size_t)lt * 16;
+            // the XCD this workgroup runs on (gfx950 XCC_ID, bits 3:0)
+            const unsigned xcc = __builtin_amdgcn_s_getreg(kHwRegXccId) & 15u;
+            if (half == 0) {
+                // written through to the device's coherence point (sc1, the
+                // agent-scope store), each 64 lanes' chunks 1 KiB contiguous
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        v4f v;
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) v[u] = wk == 0 ? facc[0][j][4 * q + u] : facc[1][j][4 * q + u];
+                        asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(slot + (j * 4 + q) * 64), "v"(v)
+                                     : "memory");
+                    }
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // every partial store of this wave has completed
+                __syncthreads();
+                // the flag tells the partner where the sums were written from
+                if (tid == 0)
+                    __hip_atomic_store(flag, 1u + xcc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return;
+            }
+            __shared__ unsigned int ready;
+            if (tid == 0) {
+                unsigned spins = 0;
+                unsigned v = 0;
+                while ((v = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0 &&
+                       ++spins < kSplitSpinLimit)
+                    __builtin_amdgcn_s_sleep(1);
+                ready = v;
+                if (v) __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __syncthreads();
+            const unsigned rv = ready;
+            // All 4 TN chunks in flight at once.  From the partner's own XCD
+            // the sums are in this L2 (a write-through store updates it):
+            // loads that skip only the CU's cache (sc0); from another XCD,
+            // loads at the coherence point (sc1, the agent-scope load).
+            // (One statement issues the loads and waits for them, so that no
+            // destination register is read or moved before its data landed.)
+            v4f buf[8];
+            const v4f* s0 = slot;
+            const v4f* s1 = slot + 4 * 64;  // chunks 4..7: 4 KiB on (immediate offsets stop at 4095)
+#define WQ_LOAD4(CP, O0, O1, O2, O3, B)                               \
+    "global_load_dwordx4 %" #O0 ", %" #B ", off " CP "\n\t"           \
+    "global_load_dwordx4 %" #O1 ", %" #B ", off offset:1024 " CP "\n\t" \
+    "global_load_dwordx4 %" #O2 ", %" #B ", off offset:2048 " CP "\n\t" \
+    "global_load_dwordx4 %" #O3 ", %" #B ", off offset:3072 " CP "\n\t"
+            if constexpr (TN == 1) {
+                if (rv == 1u + xcc)
+                    asm volatile(WQ_LOAD4("sc0", 0, 1, 2, 3, 4) "s_waitcnt vmcnt(0)"
+                                 : "=&v"(buf[0]), "=&v"(buf[1]), "=&v"(buf[2]), "=&v"(buf[3])
+                                 : "v"(s0)
+                                 : "memory");
+                else
+                    asm volatile(WQ_LOAD4("sc1", 0, 1, 2, 3, 4) "s_waitcnt vmcnt(0)"
+                                 : "=&v"(buf[0]), "=&v"(buf[1]), "=&v"(buf[2]), "=&v"(buf[3])
+                                 : "v"(s0)
+                                 : "memory");
+            } else {
+                if (rv == 1u + xcc)
+                    asm volatile(WQ_LOAD4("sc0", 0, 1, 2, 3, 8) WQ_LOAD4("sc0", 4, 5, 6, 7, 9) "s_waitcnt vmcnt(0)"
+                                 : "=&v"(buf[0]), "=&v"(buf[1]), "=&v"(buf[2]), "=&v"(buf[3]), "=&v"(buf[4]),
+                                   "=&v"(buf[5]), "=&v"(buf[6]), "=&v"(buf[7])
+                                 : "v"(s0), "v"(s1)
+                                 : "memory");
+                else
+                    asm volatile(WQ_LOAD4("sc1", 0, 1, 2, 3, 8) WQ_LOAD4("sc1", 4, 5, 6, 7, 9) "s_waitcnt vmcnt(0)"
+                                 : "=&v"(buf[0]), "=&v"(buf[1]), "=&v"(buf[2]), "=&v"(buf[3]), "=&v"(buf[4]),
+                                   "=&v"(buf[5]), "=&v"(buf[6]), "=&v"(buf[7])
+                                 : "v"(s0), "v"(s1)
+                                 : "memory");
+            }
+#undef WQ_LOAD4
+            const bool timed_out = rv == 0;
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int r = 4 * q + u;
+                        const float v = timed_out ? __builtin_nanf("") : buf[j * 4 + q][u];
+                        if (wk == 0) facc[0][j][r] = v + facc[0][j][r];
+                        else facc[1][j][r] = v + facc[1][j][r];
+                    }
+        }
+    }
+
     // epilogue: per-token scale and output mode in registers, then each
     // 32 x 32 subtile goes through a per-wave LDS transpose so that every lane
     // stores 16 consecutive bytes of a row (8 lanes cover a 128-byte row
@@ -840,7 +975,7 @@ __global__ __launch_bounds__(gemm_threads(G, PT)) void gemm_kernel(GemmParams p)
 
 template <int BN, int G, bool PT, bool DUMP>
 hipError_t launch_mode(const GemmParams& gp, hipStream_t s) {
-    dim3 grid((unsigned)(gp.tilesM * gp.tilesN)), block(gemm_threads(G, PT));
+    dim3 grid((unsigned)(gp.tilesM * gp.tilesN * (gp.split ? 2 : 1))), block(gemm_threads(G, PT));
     switch (gp.a.mode) {
         case 0: hipLaunchKernelGGL((gemm_kernel<BN, G, PT, 0, DUMP>), grid, block, 0, s, gp); break;
         case 1: hipLaunchKernelGGL((gemm_kernel<BN, G, PT, 1, DUMP>), grid, block, 0, s, gp); break;
@@ -854,8 +989,21 @@ hipError_t launch_mode(const GemmParams& gp, hipStream_t s) {
     return hipGetLastError();
 }
 
+int64_t tiles_of(const LinearArgs& a, int bn) {
+    const int64_t outw = a.mode == 2 ? bn / 2 : bn;
+    return ((a.M + kBM - 1) / kBM) * ((a.N + outw - 1) / outw);
+}
+
+// Workspace of a split launch: one 64-byte flag line per tile, then (256-byte
+// aligned) each tile's 128 x bn partial sums.
+size_t split_flag_bytes(int64_t tiles) { return (((size_t)tiles * 64) + 255) / 256 * 256; }
+size_t split_bytes(const LinearArgs& a, int bn) {
+    const int64_t t = tiles_of(a, bn);
+    return split_flag_bytes(t) + (size_t)t * kBM * bn * 4;
+}
+
 template <int BN, bool DUMP>
-hipError_t launch_tile(const LinearArgs& a, hipStream_t s) {
+hipError_t launch_tile(const LinearArgs& a, hipStream_t s, bool split = false) {
     GemmParams gp{};
     gp.a = a;
     const bool pt = a.GA == a.K;
@@ -865,6 +1013,12 @@ hipError_t launch_tile(const LinearArgs& a, hipStream_t s) {
     gp.tilesN = (int)((a.N + outw - 1) / outw);
     gp.NE = (int)(a.K / ge);
     gp.NG = (int)(a.K / a.G);
+    if (split) {
+        gp.split = 1;
+        gp.flags = static_cast<unsigned int*>(a.workspace);
+        gp.part = reinterpret_cast<float*>(static_cast<unsigned char*>(a.workspace) +
+                                           split_flag_bytes((int64_t)gp.tilesM * gp.tilesN));
+    }
     if (a.G == 128 && pt) return launch_mode<BN, 128, true, DUMP>(gp, s);
     if (a.G == 32 && pt) return launch_mode<BN, 32, true, DUMP>(gp, s);
     // the group-sum dump of the other formats runs widths up to 128 only
@@ -886,36 +1040,76 @@ hipError_t launch_tile(const LinearArgs& a, hipStream_t s) {
 // (19.3 -> 15.1 us) and 192 at M = 2048 (52.0 -> 43.1 us) and the same
 // width elsewhere.  Mode 2 needs gate/up subtile pairs per wave: widths 256
 // or 128.
-int pick_bn(const LinearArgs& a) {
-    constexpr int64_t kCu = 256, kC0 = 63;
-    const int64_t tm = (a.M + kBM - 1) / kBM;
+//
+// With K split across a workgroup pair (per-token formats, widths up to 128,
+// K a multiple of 512 with 32 steps or more, a workspace), the same model
+// extended by the K steps: a workgroup's time is c0 + steps x (ca + cb x BN)
+// (c0 3.2 us of prologue and epilogue, ca 0.131 us per step of activation
+// staging, cb 0.00525 us per step and column: a fit of the launches above and
+// of K = 6144, N = 2048 at width 64, 25.6 us), a split workgroup running half
+// the steps plus ~3 us for the exchange (measured: M = 512 and 256, K = 6144,
+// N = 2048 at width 64 split: 18.3 and 17.3 us against 24.5 and 24.1 us
+// unsplit; M = 1024 at width 128 split: 25.9 against 26.2 us at width 64).  It splits where the unsplit grid
+// leaves CUs idle: M = 1024, K = 6144, N = 2048 (width 128 in 256 pairs of
+// halves instead of 256 tiles of width 64), and the M = 256 / 512 prefills.
+struct Plan {
+    int bn;
+    bool split;
+};
+
+Plan pick_plan(const LinearArgs& a, bool allow_split) {
+    constexpr int64_t kCu = 256;
+    constexpr double kC0 = 3.2, kCa = 0.131, kCb = 0.00525, kExchange = 3.0;
+    const double steps = (double)(a.K / kBK);
     static const int widths[] = {256, 192, 128, 64};
-    int best = 64;
-    int64_t best_cost = -1;
+    Plan best{64, false};
+    double best_cost = -1.0;
     for (int bn : widths) {
         if (a.mode == 2 && bn != 256 && bn != 128) continue;
-        const int64_t outw = a.mode == 2 ? bn / 2 : bn;
-        const int64_t tiles = tm * ((a.N + outw - 1) / outw);
-        const int64_t cost = ((tiles + kCu - 1) / kCu) * (kC0 + bn);
-        if (best_cost < 0 || cost < best_cost) {
-            best = bn;
-            best_cost = cost;
+        const int64_t tiles = tiles_of(a, bn);
+        for (int sp = 0; sp < (allow_split && bn <= 128 ? 2 : 1); ++sp) {
+            const int64_t wgs = tiles * (sp ? 2 : 1);
+            const double rounds = (double)((wgs + kCu - 1) / kCu);
+            const double cost = rounds * (kC0 + (sp ? kExchange : 0.0) + steps / (sp ? 2 : 1) * (kCa + kCb * bn));
+            if (best_cost < 0 || cost < best_cost) {
+                best = Plan{bn, sp != 0};
+                best_cost = cost;
+            }
         }
     }
     return best;
 }
 
+// the shapes whose K the pair can split: per-token activations at group 128
+// or 32 (the formats with two wave groups), an even number of steps per half
+bool split_shape(const LinearArgs& a) {
+    return a.GA == a.K && (a.G == 128 || a.G == 32) && a.K % 512 == 0 && a.K / kBK >= 32;
+}
+
 template <bool DUMP>
 hipError_t launch_bn(const LinearArgs& a, hipStream_t s) {
-    switch (pick_bn(a)) {
+    Plan pl{64, false};
+    if (!DUMP && split_shape(a)) {
+        pl = pick_plan(a, true);
+        if (pl.split && !(a.workspace && a.workspace_bytes >= split_bytes(a, pl.bn))) pl = pick_plan(a, false);
+    } else {
+        pl = pick_plan(a, false);
+    }
+    switch (pl.bn) {
         case 256: return launch_tile<256, DUMP>(a, s);
         case 192: return launch_tile<192, DUMP>(a, s);
-        case 128: return launch_tile<128, DUMP>(a, s);
-        default: return launch_tile<64, DUMP>(a, s);
+        case 128: return launch_tile<128, DUMP>(a, s, pl.split);
+        default: return launch_tile<64, DUMP>(a, s, pl.split);
     }
 }
 
 }  // namespace
+
+size_t gemm_workspace_bytes(const LinearArgs& a) {
+    if (!split_shape(a)) return 0;
+    const Plan pl = pick_plan(a, true);
+    return pl.split ? split_bytes(a, pl.bn) : 0;
+}
 
 // The group-sum dump (a test hook) of the per-token group-128 format runs the
 // tile width the production launch picks for the same shape, so the sums it

@@ -34,6 +34,10 @@ struct LinearArgs {
     // nullable (the GEMM only): device wq_params {pos, seq_len, m, slot}; when
     // set, M is the capacity and the kernel covers min(m, M) tokens
     const uint32_t* params;
+    // nullable (the GEMM only): caller workspace of a K-split launch (ready
+    // flags, zero between calls, and partial sums)
+    void* workspace;
+    size_t workspace_bytes;
 };
 // word index of wq_params fields
 constexpr int kParamPos = 0;
@@ -122,6 +126,9 @@ hipError_t launch_gemv_mfma(const LinearArgs& a, const ArgmaxArgs* am, hipStream
 hipError_t launch_gemv_quant_in(const LinearArgs& a, const QuantInArgs& q, hipStream_t s);
 hipError_t launch_lm_head_argmax(const LinearArgs& a, const ArgmaxArgs& am, hipStream_t s);
 hipError_t launch_gemm(const LinearArgs& a, hipStream_t s);
+// Bytes of workspace the GEMM's K-split plan needs for this shape (0: the
+// shape never splits).
+size_t gemm_workspace_bytes(const LinearArgs& a);
 hipError_t launch_argmax(const float* logits, int64_t M, int64_t V, const uint32_t* ids,
                          uint32_t* tok_out, hipStream_t s);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);

@@ -100,7 +100,7 @@ Result<OpDef> Builder::gemv(const std::string& name, const std::string& w, uint3
 }
 
 Result<OpDef> Builder::gemm(const std::string& name, const std::string& w, uint32_t k, uint32_t n, uint32_t mode,
-                            uint32_t m, const Acts& a, Buffer y, const Buffer* params) {
+                            uint32_t m, const Acts& a, Buffer y, const Buffer* params, const Buffer* workspace) {
     std::string e = check_kn(name, k, n, mode);
     if (e.empty() && m == 0) e = fmt("%s: 0 tokens", name.c_str());
     if (e.empty()) e = check_acts(name, k, m, a);
@@ -113,10 +113,11 @@ Result<OpDef> Builder::gemm(const std::string& name, const std::string& w, uint3
     const int32_t g = group_, ga = (int32_t)(a.ga == 0 ? k : a.ga);
     const Acts in = a;
     const wq_params* pp = params ? (const wq_params*)params->ptr : nullptr;
+    const Buffer wsb = workspace ? *workspace : Buffer{};
     return Result<OpDef>::ok(OpDef{name, [=](void* s, Step st) {
         return wq_gemm(s, (const uint32_t*)q.q.ptr, (const uint32_t*)q.s.ptr, n, k, g, (const int8_t*)in.xq.ptr,
                        (const float*)in.dx.ptr, (const int32_t*)in.xs.ptr, step_tokens(st, m), ga, (int32_t)mode,
-                       (float*)y.ptr, pp);
+                       (float*)y.ptr, pp, wsb.ptr, wsb.bytes);
     }});
 }
 

@@ -103,9 +103,12 @@ class Builder {
     // the prefill product over up to m tokens (graph.rs:200-205); params
     // (optional): the step's Params buffer (wq_params, 16 bytes of device
     // memory) the kernel reads when it runs, so the tokens it covers follow
-    // the buffer's m (at most m, the capacity the buffers hold)
+    // the buffer's m (at most m, the capacity the buffers hold); workspace
+    // (optional, zeroed once): wq_gemm_workspace_bytes for the shape, so that
+    // the library may split K between workgroup pairs
     Result<OpDef> gemm(const std::string& name, const std::string& w, uint32_t k, uint32_t n, uint32_t mode,
-                       uint32_t m, const Acts& a, Buffer y, const Buffer* params = nullptr);
+                       uint32_t m, const Acts& a, Buffer y, const Buffer* params = nullptr,
+                       const Buffer* workspace = nullptr);
     // GEMM for Prefill, GEMV otherwise (graph.rs:207-214); m: the prefill
     // tokens (the other paths take theirs from the path); params as gemm's
     Result<OpDef> matmul(Path path, const std::string& name, const std::string& w, uint32_t k, uint32_t n,

@@ -216,7 +216,7 @@ def _check_params(params, device):
     return _check(params, "params", _ID_DTYPES, shape=(4,), device=device)
 
 
-def _linear(fn, w: Q4Tensor, a: Acts, mode, y, stream, acc=None, params=None, pass_params=False):
+def _linear(fn, w: Q4Tensor, a: Acts, mode, y, stream, acc=None, params=None, pass_params=False, workspace=None):
     _check_linear(w, a)
     N = _nrows(w, mode)
     _check_params(params, a.xq.device)
@@ -231,6 +231,11 @@ def _linear(fn, w: Q4Tensor, a: Acts, mode, y, stream, acc=None, params=None, pa
             args.append(_ptr(acc))
         if pass_params:
             args.append(_ptr(params))
+            if workspace is not None:
+                _check(workspace, "workspace", torch.uint8, device=a.xq.device)
+                args += [_ptr(workspace), workspace.numel()]
+            else:
+                args += [None, 0]
         _lib.call(fn, *args)
     return y
 
@@ -267,11 +272,22 @@ def quant_gemv(w: Q4Tensor, x, norm=None, eps=1e-6, mode=MODE_STORE, y=None, out
     return y, a
 
 
-def gemm(w: Q4Tensor, a: Acts, mode=MODE_STORE, y=None, stream=None, params=None):
+def gemm(w: Q4Tensor, a: Acts, mode=MODE_STORE, y=None, stream=None, params=None, workspace=None):
     """Prefill GEMM on int8 MFMA (Builder::gemm, gemm_q4q8.wgsl).  params
     (make_params, optional): a.M is then the capacity and the kernel covers
-    the params' m tokens, read when it runs; rows past them are not written."""
-    return _linear("wq_gemm", w, a, mode, y, stream, params=params, pass_params=True)
+    the params' m tokens, read when it runs; rows past them are not written.
+    workspace (gemm_workspace, optional): lets the library split K between
+    workgroup pairs on the shapes where that pays."""
+    return _linear("wq_gemm", w, a, mode, y, stream, params=params, pass_params=True, workspace=workspace)
+
+
+def gemm_workspace(N, K, G, M, GA=None, mode=MODE_STORE, device="cuda"):
+    """A zeroed uint8 workspace of wq_gemm_workspace_bytes for this shape (a
+    one-byte tensor when the shape never splits); reusable by later calls of
+    the same or a smaller shape, not by overlapping ones."""
+    nbytes = int(_lib.load().wq_gemm_workspace_bytes(N, K, G, M, K if GA is None else GA, mode))
+    # 256-byte aligned: the caching allocator hands out 512-byte aligned blocks
+    return torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
 
 
 def matmul(path, w: Q4Tensor, a: Acts, mode=MODE_STORE, y=None, stream=None, params=None):
