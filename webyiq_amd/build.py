@@ -45,6 +45,10 @@ CFLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
+# Per-source flags.  gemv_q4q8.hip: its kernel's nine leading arguments (14
+# SGPRs: what the first global loads need) are preloaded into SGPRs at wave
+# launch (no scalar load of the argument segment before the first load).
+SOURCE_FLAGS = {"gemv_q4q8.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"]}
 # what the host pass prints for the device-only feature above (harmless)
 HOST_PASS_NOTE = "'-packed-fp32-ops' is not a recognized feature for this target (ignoring feature)"
 
@@ -56,12 +60,13 @@ def build(verbose=False):
     for src in SOURCES:
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmd = [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+        cmd = [HIPCC, *CFLAGS, *SOURCE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
     tl_obj = os.path.join(BUILD, "gemv_q4q8_timeline.o")
-    cmd = [HIPCC, *CFLAGS, "-DWQ_TIMELINE", "-c", os.path.join(CSRC, TIMELINE_SOURCE), "-o", tl_obj]
+    cmd = [HIPCC, *CFLAGS, *SOURCE_FLAGS.get(TIMELINE_SOURCE, []), "-DWQ_TIMELINE", "-c",
+           os.path.join(CSRC, TIMELINE_SOURCE), "-o", tl_obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     procs.append((TIMELINE_SOURCE + " (timeline)", subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))

@@ -81,23 +81,43 @@ __device__ __forceinline__ T* lds_align(unsigned char* base, const void* p) {
 }
 
 template <int MT, int MODE, int G, bool PT, int IPW, bool ARGMAX, bool QIN>
-__global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
+// Everything the first global loads need leads the argument list as separate
+// arguments: the weight, activation, weight-scale and activation-scale
+// pointers, N, K, two words packing the plan (RB | nslots << 8 | J << 12 |
+// M << 16, and NG | NE << 16) and the activation sums.  This translation unit
+// is built with -amdgpu-kernarg-preload-count=9, so these 14 SGPRs (the user
+// SGPRs left beside the argument segment's address) arrive with the wave
+// instead of through a scalar load of the argument segment that every wave
+// would wait for before its first load (probe kernels of the headline GEMV's
+// shape: 0.2-0.33 us per launch).  The output pointer follows them; the
+// parameter struct carries the same values and the rest, read after the loads
+// are issued.
+__global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const int8_t* kxq, const uint32_t* kws,
+                                                   const float* kdx, int kN, int kK, uint32_t kplan, uint32_t kgroups,
+                                                   const int32_t* kxs, float* ky, GemvParams pk) {
     constexpr int GE = PT ? G : 32;        // accumulation group
     constexpr int LPG = GE / 32;           // lanes per accumulation group (1 or 4)
     constexpr int LPW = G / 32;            // lanes per weight group (1 or 4)
     constexpr int NH = MODE == 2 ? 2 : 1;  // gate (+ up) row halves
     extern __shared__ __align__(16) unsigned char smem[];
 
+    GemvParams p = pk;
+    p.a.wq = kwq;
+    p.a.ws = kws;
+    p.a.xq = kxq;
+    p.a.xs = kxs;
+    p.a.dx = kdx;
+    p.a.y = ky;
+    p.a.N = kN;
+    p.a.K = kK;
+    p.a.M = (kplan >> 16) & 255;
+    p.RB = kplan & 255;
+    p.nslots = (kplan >> 8) & 15;
+    p.J = (kplan >> 12) & 15;
+    p.NG = kgroups & 0xFFFF;
+    p.NE = kgroups >> 16;
     const LinearArgs& a = p.a;
-    // every kernel argument in SGPRs before the first global load
-    pin_arg(a.wq); pin_arg(a.ws); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs); pin_arg(a.y);
-    pin_arg(a.acc_dump); pin_arg(a.N); pin_arg(a.K); pin_arg(a.M);
-    pin_arg(p.J); pin_arg(p.nslots); pin_arg(p.RB); pin_arg(p.NE); pin_arg(p.NEP); pin_arg(p.NG);
-    if (ARGMAX) {
-        pin_arg(p.am.ids); pin_arg(p.am.tok_out); pin_arg(p.am.keys); pin_arg(p.am.ticket);
-        pin_arg(p.nblocks);
-    }
-    if (QIN) {
+    if (QIN) {  // the fused quantiser's input is loaded first
         pin_arg(p.qin.x); pin_arg(p.qin.norm_w); pin_arg(p.qin.eps);
         pin_arg(p.qin.xq); pin_arg(p.qin.dx); pin_arg(p.qin.xs);
     }
@@ -112,7 +132,8 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     const int64_t N = a.N;
     const int K = (int)a.K;
     const int RB = p.RB;
-    const int NE = p.NE, NEP = p.NEP, NG = p.NG;
+    const int NE = p.NE, NG = p.NG;
+    const int NEP = (NE + 4) & ~3;  // the plan's padded stride (make_plan), from a preloaded value
     const int NGS = NG + 2;  // LDS row stride of the (s, m) pairs: rows on distinct banks
     const int NDX = PT ? 1 : K / 32;
     const int64_t r0 = (int64_t)blockIdx.x * RB;
@@ -213,6 +234,13 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
             sv[h][s] = a.ws[(row + h * N) * NG + g];
         }
         asm volatile("" ::: "memory");  // loads stay in row order: row s lands before row s + 1
+    }
+    // the arguments read later, in SGPRs now that the loads are in flight
+    // (a scalar load sunk next to a late use would add a round trip there)
+    pin_arg(a.acc_dump);
+    if (ARGMAX) {
+        pin_arg(p.am.ids); pin_arg(p.am.tok_out); pin_arg(p.am.keys); pin_arg(p.am.ticket);
+        pin_arg(p.nblocks);
     }
     if constexpr (!QIN) {
         WQ_STAMP(1, xa[0].x ^ xb[0].w ^ (uint32_t)xsv[0] ^ __float_as_uint(dxv[0]));
@@ -761,14 +789,22 @@ Plan make_plan(const LinearArgs& a, bool argmax, bool qin = false) {
 template <int MT, int MODE, int G, bool PT, bool ARGMAX, bool QIN>
 hipError_t launch_ipw(const Plan& pl, const GemvParams& gp, hipStream_t s) {
     dim3 grid(pl.grid), block(64 * pl.waves);
+    const LinearArgs& a = gp.a;
+    // the preloaded arguments (gemv_kernel): plan fields packed in two words
+    const uint32_t plan = (uint32_t)gp.RB | ((uint32_t)gp.nslots << 8) | ((uint32_t)gp.J << 12) | ((uint32_t)a.M << 16);
+    const uint32_t groups = (uint32_t)gp.NG | ((uint32_t)gp.NE << 16);
+#define WQ_GEMV_LAUNCH(IPW)                                                                                 \
+    hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, IPW, ARGMAX, QIN>), grid, block, pl.lds, s, a.wq, a.xq, \
+                       a.ws, a.dx, (int)a.N, (int)a.K, plan, groups, a.xs, a.y, gp)
     switch (pl.IPW) {
-        case 1: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 1, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
-        case 2: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 2, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
-        case 3: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 3, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
-        case 4: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 4, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
-        case 6: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 6, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
-        default: hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, 8, ARGMAX, QIN>), grid, block, pl.lds, s, gp); break;
+        case 1: WQ_GEMV_LAUNCH(1); break;
+        case 2: WQ_GEMV_LAUNCH(2); break;
+        case 3: WQ_GEMV_LAUNCH(3); break;
+        case 4: WQ_GEMV_LAUNCH(4); break;
+        case 6: WQ_GEMV_LAUNCH(6); break;
+        default: WQ_GEMV_LAUNCH(8); break;
     }
+#undef WQ_GEMV_LAUNCH
     return hipGetLastError();
 }
 
