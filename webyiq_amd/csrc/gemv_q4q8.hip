@@ -83,8 +83,10 @@ __device__ __forceinline__ T* lds_align(unsigned char* base, const void* p) {
 template <int MT, int MODE, int G, bool PT, int IPW, bool ARGMAX, bool QIN>
 // Everything the first global loads need leads the argument list as separate
 // arguments: the weight, activation, weight-scale and activation-scale
-// pointers, N, K, two words packing the plan (RB | nslots << 8 | J << 12 |
-// M << 16, and NG | NE << 16) and the activation sums.  This translation unit
+// pointers (with the fused quantiser: its f32 input and norm weight in the
+// activation and activation-scale slots), N, K, two words packing the plan
+// (RB | nslots << 8 | J << 12 | M << 16, and NG | NE << 16) and the
+// activation sums.  This translation unit
 // is built with -amdgpu-kernarg-preload-count=9, so these 14 SGPRs (the user
 // SGPRs left beside the argument segment's address) arrive with the wave
 // instead of through a scalar load of the argument segment that every wave
@@ -104,9 +106,14 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
     GemvParams p = pk;
     p.a.wq = kwq;
     p.a.ws = kws;
-    p.a.xq = kxq;
+    if (QIN) {  // the fused quantiser's f32 input and norm weight take the activation slots
+        p.qin.x = reinterpret_cast<const float*>(kxq);
+        p.qin.norm_w = kdx;
+    } else {
+        p.a.xq = kxq;
+        p.a.dx = kdx;
+    }
     p.a.xs = kxs;
-    p.a.dx = kdx;
     p.a.y = ky;
     p.a.N = kN;
     p.a.K = kK;
@@ -117,10 +124,6 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
     p.NG = kgroups & 0xFFFF;
     p.NE = kgroups >> 16;
     const LinearArgs& a = p.a;
-    if (QIN) {  // the fused quantiser's input is loaded first
-        pin_arg(p.qin.x); pin_arg(p.qin.norm_w); pin_arg(p.qin.eps);
-        pin_arg(p.qin.xq); pin_arg(p.qin.dx); pin_arg(p.qin.xs);
-    }
     const int tid = threadIdx.x;
     WQ_STAMP(0, 0u);
     const int lane = tid & 63;
@@ -238,6 +241,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
     // the arguments read later, in SGPRs now that the loads are in flight
     // (a scalar load sunk next to a late use would add a round trip there)
     pin_arg(a.acc_dump);
+    if (QIN) { pin_arg(p.qin.eps); pin_arg(p.qin.xq); pin_arg(p.qin.dx); pin_arg(p.qin.xs); }
     if (ARGMAX) {
         pin_arg(p.am.ids); pin_arg(p.am.tok_out); pin_arg(p.am.keys); pin_arg(p.am.ticket);
         pin_arg(p.nblocks);
@@ -793,9 +797,11 @@ hipError_t launch_ipw(const Plan& pl, const GemvParams& gp, hipStream_t s) {
     // the preloaded arguments (gemv_kernel): plan fields packed in two words
     const uint32_t plan = (uint32_t)gp.RB | ((uint32_t)gp.nslots << 8) | ((uint32_t)gp.J << 12) | ((uint32_t)a.M << 16);
     const uint32_t groups = (uint32_t)gp.NG | ((uint32_t)gp.NE << 16);
+    const int8_t* xq_slot = QIN ? reinterpret_cast<const int8_t*>(gp.qin.x) : a.xq;
+    const float* dx_slot = QIN ? gp.qin.norm_w : a.dx;
 #define WQ_GEMV_LAUNCH(IPW)                                                                                 \
-    hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, IPW, ARGMAX, QIN>), grid, block, pl.lds, s, a.wq, a.xq, \
-                       a.ws, a.dx, (int)a.N, (int)a.K, plan, groups, a.xs, a.y, gp)
+    hipLaunchKernelGGL((gemv_kernel<MT, MODE, G, PT, IPW, ARGMAX, QIN>), grid, block, pl.lds, s, a.wq, xq_slot, \
+                       a.ws, dx_slot, (int)a.N, (int)a.K, plan, groups, a.xs, a.y, gp)
     switch (pl.IPW) {
         case 1: WQ_GEMV_LAUNCH(1); break;
         case 2: WQ_GEMV_LAUNCH(2); break;

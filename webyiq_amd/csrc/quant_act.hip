@@ -84,11 +84,11 @@ __device__ __forceinline__ void emit(const QuantArgs& a, int64_t t, int c, bool 
 // eight each holds one chunk and they meet as ((s0 + s1) + (s2 + s3)) +
 // ((s4 + s5) + (s6 + s7)).
 template <bool NORM, bool PER_TOKEN, int GE, int QW>
-__global__ __launch_bounds__(64 * QW) void quant_split_kernel(QuantArgs a) {
+__global__ __launch_bounds__(64 * QW) void quant_split_kernel(const float* kx, const float* knw, int kK, int kM,
+                                                              QuantArgs a) {
     static_assert(QW == 4 || QW == 8, "waves per token");
     constexpr int LPW = 8 / QW;  // loads per wave and pass
-    pin_arg(a.x); pin_arg(a.norm_w); pin_arg(a.eps); pin_arg(a.K);
-    pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
+    a.x = kx; a.norm_w = knw; a.K = kK; a.M = kM;  // preloaded (leading arguments)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t t = blockIdx.x;
     const int K = (int)a.K;
@@ -109,9 +109,16 @@ __global__ __launch_bounds__(64 * QW) void quant_split_kernel(QuantArgs a) {
         for (int i = 0; i < LPW; ++i) {
             const int c = chunk(j, i);
             const bool ok = j < J && c < nchunk;
-            xc[j][i] = ok ? xr[c] : zero4;
-            if (NORM) wc[j][i] = ok ? nw[c] : zero4;
+            const int cc = ok ? c : 0;  // loads from a valid chunk, no branch
+            const float4 xv = xr[cc];
+            xc[j][i] = ok ? xv : zero4;
+            if (NORM) {
+                const float4 wv = nw[cc];
+                wc[j][i] = ok ? wv : zero4;
+            }
         }
+    // the outputs and epsilon, in SGPRs once the loads are in flight
+    pin_arg(a.eps); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
 
     float r = 1.0f;
     if (NORM) {
@@ -174,9 +181,9 @@ __global__ __launch_bounds__(64 * QW) void quant_split_kernel(QuantArgs a) {
 // rows of at most JC passes stay in registers; JC == 0: longer rows are
 // re-read (L2 hits) in each phase.
 template <bool NORM, bool PER_TOKEN, int GE, int JC>
-__global__ __launch_bounds__(kQuantThreads) void quant_wave_kernel(QuantArgs a) {
-    pin_arg(a.x); pin_arg(a.norm_w); pin_arg(a.eps); pin_arg(a.K); pin_arg(a.M);
-    pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
+__global__ __launch_bounds__(kQuantThreads) void quant_wave_kernel(const float* kx, const float* knw, int kK, int kM,
+                                                                   QuantArgs a) {
+    a.x = kx; a.norm_w = knw; a.K = kK; a.M = kM;  // preloaded (leading arguments)
     const int lane = threadIdx.x & 63;
     const int64_t t = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
     if (t >= a.M) return;  // whole wavefronts; the kernel has no barrier
@@ -197,10 +204,17 @@ __global__ __launch_bounds__(kQuantThreads) void quant_wave_kernel(QuantArgs a) 
             for (int u = 0; u < 8; ++u) {
                 const int c = chunk(j, u);
                 const bool ok = j < J && c < nchunk;
-                xc[j][u] = ok ? xr[c] : zero4;
-                if (NORM) wc[j][u] = ok ? nw[c] : zero4;
+                const int cc = ok ? c : 0;  // loads from a valid chunk, no branch
+                const float4 xv = xr[cc];
+                xc[j][u] = ok ? xv : zero4;
+                if (NORM) {
+                    const float4 wv = nw[cc];
+                    wc[j][u] = ok ? wv : zero4;
+                }
             }
     }
+    // the outputs and epsilon, in SGPRs once the loads are in flight
+    pin_arg(a.eps); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
     auto raw = [&](int j, int u) -> float4 {
         if (JC > 0) return xc[JC > 0 ? j : 0][u];
         const int c = chunk(j, u);
@@ -442,16 +456,19 @@ hipError_t dispatch_rows(const QuantArgs& a, hipStream_t s) {
 #define WQ_QUANT_SPLIT_WAVES 8
 #endif
         hipLaunchKernelGGL((quant_split_kernel<NORM, PT, GE, WQ_QUANT_SPLIT_WAVES>), dim3((unsigned)a.M),
-                           dim3(64 * WQ_QUANT_SPLIT_WAVES), 0, s, a);
+                           dim3(64 * WQ_QUANT_SPLIT_WAVES), 0, s, a.x, a.norm_w, (int)a.K, (int)a.M, a);
         return hipGetLastError();
     }
     dim3 grid((unsigned)((a.M + kQuantWaves - 1) / kQuantWaves)), block(kQuantThreads);
     if (passes <= 1)
-        hipLaunchKernelGGL((quant_wave_kernel<NORM, PT, GE, 1>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((quant_wave_kernel<NORM, PT, GE, 1>), grid, block, 0, s, a.x, a.norm_w, (int)a.K,
+                           (int)a.M, a);
     else if (passes <= 3)
-        hipLaunchKernelGGL((quant_wave_kernel<NORM, PT, GE, 3>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((quant_wave_kernel<NORM, PT, GE, 3>), grid, block, 0, s, a.x, a.norm_w, (int)a.K,
+                           (int)a.M, a);
     else
-        hipLaunchKernelGGL((quant_wave_kernel<NORM, PT, GE, 0>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((quant_wave_kernel<NORM, PT, GE, 0>), grid, block, 0, s, a.x, a.norm_w, (int)a.K,
+                           (int)a.M, a);
     return hipGetLastError();
 }
 
