@@ -51,49 +51,69 @@ __device__ __forceinline__ int group_sum(int v) {
     return v;
 }
 
+// The leading arguments are what the first loads need (the partials, the
+// Params pointer, H, nch and the host's position bound); this translation
+// unit preloads them into SGPRs (-amdgpu-kernarg-preload-count=5), so no
+// scalar load of the argument segment precedes the first loads.
 template <int DPL>
-__global__ __launch_bounds__(64 * kCombineWaves) void attn_combine_kernel(AttnCombineArgs a) {
-    pin_arg(a.part); pin_arg(a.M); pin_arg(a.H); pin_arg(a.nch); pin_arg(a.pos); pin_arg(a.params);
-    pin_arg(a.gate); pin_arg(a.gate_stride); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
+__global__ __launch_bounds__(64 * kCombineWaves) void attn_combine_kernel(const float* kpart, const uint32_t* kparams,
+                                                                          int kH, int knch, int kpos,
+                                                                          AttnCombineArgs a) {
+    a.part = kpart; a.params = kparams; a.H = kH; a.nch = knch; a.pos = kpos;
     constexpr int D = 64 * DPL;
     constexpr int LPG = 32 / DPL;  // lanes per 32-dim group
     constexpr int UNROLL = 8;      // chunks in flight per wavefront
     extern __shared__ float sh[];  // chunk weights [nch] | chains of waves 1..3 [3][D]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t item = blockIdx.x;  // m * H + h
-    const int64_t m = item / a.H, h = item - m * a.H;
+    const int item = (int)blockIdx.x;  // m * H + h (M <= 64, H <= 1024: checked on the host)
+    const int m = item / kH, h = item - m * kH;
     const int nch = (int)a.nch;
-    // the step's position: the host's, or the device Params' (clamped to the
-    // host bound, so that n <= nch whatever the buffer holds)
-    int64_t pos = a.pos;
-    if (a.params) {
-        const int64_t p = (int64_t)a.params[kParamPos];
-        pos = p < a.pos ? p : a.pos;
-    }
-    const int n = (int)((pos + m + kChunk) / kChunk);  // <= nch (checked on the host)
-    const float* hb = a.part + item * (int64_t)nch * (D + 2);
+    // n_hi: the chunk count at the host's bound, n: at the step's position
+    const int n_hi = (kpos + m + kChunk) / kChunk;  // <= nch (checked on the host)
+    const float* hb = a.part + (int64_t)item * nch * (D + 2);
     float* w = sh;
     float* chains = sh + nch;
 
-    // The partials of this wave's first UNROLL chunks and (wave 0) the first
-    // weight sums do not depend on the maximum: their loads are issued with
-    // the maxima's, one memory round trip instead of two.
+    // The partials of this wave's first UNROLL chunks, the weight sum and
+    // maximum of chunk `lane` and the maximum of chunk `tid` depend neither
+    // on the maximum nor on the Params load: they are loaded up to the host's
+    // bound before the position is read, one memory round trip instead of
+    // three, and masked to the step's chunks where they are used.
     const float* pl = hb + DPL * lane;
     float pf[UNROLL][DPL];
 #pragma unroll
     for (int q = 0; q < UNROLL; ++q) {
         const int cq = wave + kCombineWaves * q;
+        const int cc = cq < n_hi ? cq : 0;  // loads from a valid chunk, no branch
 #pragma unroll
-        for (int k = 0; k < DPL; ++k) pf[q][k] = cq < n ? pl[(int64_t)cq * (D + 2) + k] : 0.0f;
+        for (int k = 0; k < DPL; ++k) {
+            const float v = pl[(int64_t)cc * (D + 2) + k];
+            pf[q][k] = cq < n_hi ? v : 0.0f;
+        }
     }
-    const float lf = wave == 0 && lane < n ? hb[(int64_t)lane * (D + 2) + D + 1] : 0.0f;
+    const int lc = lane < n_hi ? lane : 0;
+    const float lv = hb[(int64_t)lc * (D + 2) + D + 1], mv = hb[(int64_t)lc * (D + 2) + D];
+    const float m0 = lane < n_hi ? mv : -3.0e38f;
+    const int tcc = tid < n_hi ? tid : 0;
+    const float mt = hb[(int64_t)tcc * (D + 2) + D];  // chunk tid's maximum (tid < n <= n_hi where used)
+    asm volatile("" ::: "memory");  // the Params read below stays behind these loads
+    const uint32_t p_dev = a.params ? a.params[kParamPos] : 0xFFFFFFFFu;
+    // the rest of the arguments, in SGPRs once the loads are in flight
+    pin_arg(a.M); pin_arg(a.gate); pin_arg(a.gate_stride); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs);
+
+    // the step's position: the host's, or the device Params' (clamped to the
+    // host bound, so that n <= n_hi <= nch whatever the buffer holds)
+    const int64_t pos = (int64_t)p_dev < a.pos ? (int64_t)p_dev : a.pos;
+    const int n = (int)((pos + m + kChunk) / kChunk);
 
     // chunk maxima (attn_combine.wgsl:39-42), in every wavefront
-    float ml = -3.0e38f;
-    for (int c = lane; c < n; c += 64) ml = fmaxf(ml, hb[(int64_t)c * (D + 2) + D]);
+    float ml = lane < n ? m0 : -3.0e38f;
+    for (int c = lane + 64; c < n; c += 64) ml = fmaxf(ml, hb[(int64_t)c * (D + 2) + D]);
     const float mx = wave_max(ml);
-    // chunk weights (:46), once per workgroup
-    for (int c = tid; c < n; c += 64 * kCombineWaves) w[c] = expf(hb[(int64_t)c * (D + 2) + D] - mx);
+    // chunk weights (:46), once per workgroup; chunk tid's maximum was loaded up front
+    if (tid < n) w[tid] = expf(mt - mx);
+    for (int c = tid + 64 * kCombineWaves; c < n; c += 64 * kCombineWaves)
+        w[c] = expf(hb[(int64_t)c * (D + 2) + D] - mx);
     __syncthreads();
 
     // wave w's chains over chunks w, w + 4, ... (:48)
@@ -136,7 +156,7 @@ __global__ __launch_bounds__(64 * kCombineWaves) void attn_combine_kernel(AttnCo
     // weight sum (:47), lane-parallel then the lane tree
     float ll = 0.0f;
     if (wave == 0) {
-        if (lane < n) ll = fmaf(w[lane], lf, ll);
+        if (lane < n) ll = fmaf(w[lane], lv, ll);  // lane < n <= n_hi: lv is chunk lane's
         for (int cc = lane + 64; cc < n; cc += 64) ll = fmaf(w[cc], hb[(int64_t)cc * (D + 2) + D + 1], ll);
     }
     __syncthreads();
@@ -189,9 +209,9 @@ hipError_t launch_attn_combine(const AttnCombineArgs& a, hipStream_t s) {
     dim3 grid((unsigned)(a.M * a.H)), block(64 * kCombineWaves);
     const size_t lds = ((size_t)a.nch + 3 * (size_t)a.D) * sizeof(float);
     switch (a.D) {
-        case 64: hipLaunchKernelGGL((attn_combine_kernel<1>), grid, block, lds, s, a); break;
-        case 128: hipLaunchKernelGGL((attn_combine_kernel<2>), grid, block, lds, s, a); break;
-        default: hipLaunchKernelGGL((attn_combine_kernel<4>), grid, block, lds, s, a); break;
+        case 64: hipLaunchKernelGGL((attn_combine_kernel<1>), grid, block, lds, s, a.part, a.params, (int)a.H, (int)a.nch, (int)a.pos, a); break;
+        case 128: hipLaunchKernelGGL((attn_combine_kernel<2>), grid, block, lds, s, a.part, a.params, (int)a.H, (int)a.nch, (int)a.pos, a); break;
+        default: hipLaunchKernelGGL((attn_combine_kernel<4>), grid, block, lds, s, a.part, a.params, (int)a.H, (int)a.nch, (int)a.pos, a); break;
     }
     return hipGetLastError();
 }
