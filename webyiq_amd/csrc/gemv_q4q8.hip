@@ -127,11 +127,17 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
     const int tid = threadIdx.x;
     WQ_STAMP(0, 0u);
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // The wave index and what derives from it are wave-uniform values in
+    // SGPRs: row addresses are then scalar bases plus a 32-bit lane offset,
+    // and the few dozen instructions before the last load is issued are
+    // mostly scalar (with three waves a SIMD, each vector instruction there
+    // delays the loads of all three).
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int NW = p.J * p.nslots;  // waves (blockDim.x / 64, without its late scalar load)
     const int nthreads = 64 * NW;
-    const int j = wave % p.J;
-    const int slot = wave / p.J;
+    // wave = j * nslots + slot; nslots is 1, 2 or 4 (a power of two)
+    const int slot = wave & (p.nslots - 1);
+    const int j = wave >> (p.nslots >> 1);
     const int64_t N = a.N;
     const int K = (int)a.K;
     const int RB = p.RB;
@@ -161,7 +167,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
     const int e = kpos / GE;  // this lane's accumulation group
     const int g = kpos / G;   // this lane's weight group
     const size_t row_bytes = (size_t)K / 2;
-    const unsigned char* wbase = reinterpret_cast<const unsigned char*>(a.wq) + (size_t)kpos / 2;
+    const uint32_t woff = (uint32_t)kpos / 2;  // this lane's byte offset in a packed row
 
     // 0. fused quantiser input first, coalesced and split between the
     //    nslots waves of a pass: the wave of pass j and slot s reads loads
@@ -213,12 +219,12 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
         // can then start as soon as its weights land
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-            int64_t tt = t < a.M ? t : a.M - 1;
-            const unsigned char* xp = reinterpret_cast<const unsigned char*>(a.xq) + tt * a.K + kpos;
-            xa[t] = load16(xp);
-            xb[t] = load16(xp + 16);
-            xsv[t] = a.xs[tt * NE + e];
-            dxv[t] = a.dx[tt * NDX + (PT ? 0 : e)];
+            const int tt = (t == 0 || t < (int)a.M) ? t : (int)a.M - 1;  // M >= 1
+            const unsigned char* xt = reinterpret_cast<const unsigned char*>(a.xq) + (size_t)tt * K;  // uniform
+            xa[t] = load16(xt + (uint32_t)kpos);
+            xb[t] = load16(xt + (uint32_t)kpos + 16);
+            xsv[t] = (a.xs + (size_t)tt * NE)[e];
+            dxv[t] = (a.dx + (size_t)tt * NDX)[PT ? 0 : e];
         }
         asm volatile("" ::: "memory");  // keep them ahead of the weight stream
     }
@@ -229,12 +235,15 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
     uint32_t sv[NH][IPW];
 #pragma unroll
     for (int s = 0; s < IPW; ++s) {
-        int64_t row = r0 + slot + (int64_t)p.nslots * s;
-        row = row < N ? row : N - 1;
+        // 32-bit row indices (rows * K / 2 < 4 GiB: checked on the host)
+        int row = (int)r0 + slot + p.nslots * s;
+        row = row < (int)N ? row : (int)N - 1;
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
-            wv[h][s] = load_stream16(wbase + (size_t)(row + h * N) * row_bytes);
-            sv[h][s] = a.ws[(row + h * N) * NG + g];
+            const uint32_t rh = (uint32_t)(row + h * (int)N);
+            const unsigned char* rp = reinterpret_cast<const unsigned char*>(a.wq) + (size_t)rh * row_bytes;
+            wv[h][s] = load_stream16(rp + woff);
+            sv[h][s] = (a.ws + (size_t)rh * NG)[g];
         }
         asm volatile("" ::: "memory");  // loads stay in row order: row s lands before row s + 1
     }
@@ -275,12 +284,12 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
                 float st = c[0] + c[1];
                 if (qus >= 4) st = st + (c[2] + c[3]);
                 if (qus == 8) st = st + ((c[4] + c[5]) + (c[6] + c[7]));
-                sub[(t * 8 + wave) * 64 + lane] = st;
+                sub[(t * 8 + slot * p.J + j) * 64 + lane] = st;
             }
             __syncthreads();
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
-                // pass jj's lane partials: slot s's subtree sits at wave s * J + jj;
+                // pass jj's lane partials: slot s's subtree sits at index s * J + jj;
                 // the pass sums are added in pass order (J <= 8)
                 float total = 0.0f;
 #pragma unroll
