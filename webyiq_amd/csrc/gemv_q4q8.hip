@@ -176,7 +176,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
     //    before the weight stream, so waiting for them does not wait for it.
     constexpr int QT = QIN ? MT : 1;
     float4 qx[QT][8], qw[8];
-    const int qus = 8 / p.nslots, qu0 = slot * qus;  // nslots is 1, 2 or 4: qus 8, 4 or 2
+    const int qus = 8 >> (p.nslots >> 1), qu0 = slot * qus;  // 8 / nslots: nslots is 1, 2 or 4
     // f(i) for this wave's loads i < qus; the skipped ones are branched over
     // (uniformly), not computed and discarded
     auto for_chunks = [&](auto&& f) {
@@ -198,13 +198,14 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
         const float* nsrc = p.qin.norm_w ? p.qin.norm_w : p.qin.x;  // unconditional loads
         for_chunks([&](int i) {
             const int c = 512 * j + 64 * (qu0 + i) + lane;
-            const int cc = c < nchunk ? c : 0;
+            const uint32_t cb = (uint32_t)(c < nchunk ? c : 0) * 16u;  // the chunk's byte offset in a row
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
-                const int64_t tt = t < a.M ? t : a.M - 1;
-                qx[t][i] = reinterpret_cast<const float4*>(p.qin.x + tt * a.K)[cc];
+                const int tt = (t == 0 || t < (int)a.M) ? t : (int)a.M - 1;  // M >= 1
+                const unsigned char* xt = reinterpret_cast<const unsigned char*>(p.qin.x + (size_t)tt * K);
+                qx[t][i] = *reinterpret_cast<const float4*>(xt + cb);
             }
-            qw[i] = reinterpret_cast<const float4*>(nsrc)[cc];
+            qw[i] = *reinterpret_cast<const float4*>(reinterpret_cast<const unsigned char*>(nsrc) + cb);
         });
         // keep these loads ahead of the weight stream (no sinking into their
         // use, which would wait for every weight load)
