@@ -385,20 +385,37 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
         const bool lead = kact && (lane & 3) == 0;
         const int rows_total = NH * (int)N;
         float vals[NH][IPW][MT];
+        // y of token 0, local row rl (the plain GEMV's one-token emit)
+        auto emit_row = [&](int rl, float v0, float v1, float d) {
+            const int row = (int)r0 + rl;
+            if (row < (int)N) {
+                float* yo = a.y + row;
+                const float v = v0 * d;
+                if (MODE == 0) *yo = v;
+                else if (MODE == 1) *yo = *yo + v;
+                else *yo = silu_mul(v, v1 * d);
+            }
+        };
 #pragma unroll
         for (int s = 0; s < IPW; ++s) {
-            const int64_t row = r0 + slot + p.nslots * s;
+            const int row = (int)r0 + slot + p.nslots * s;  // 32-bit: compared on the scalar unit
 #pragma unroll
             for (int h = 0; h < NH; ++h) {
                 const float ws_s = f16lo(sv[h][s]), ws_m = f16hi(sv[h][s]);
 #pragma unroll
                 for (int t = 0; t < MT; ++t) {
                     const int d = quad_sum(dot32(wv[h][s], xa[t], xb[t]));
-                    if (a.acc_dump && lead && t < a.M && row < N)  // test hook: the exact group sums
-                        a.acc_dump[((int64_t)t * rows_total + h * N + row) * NE + e] = d;
+                    if (a.acc_dump) {  // test hook (uniform branch): the exact group sums
+                        if (lead && t < (int)a.M && row < (int)N)
+                            a.acc_dump[((int64_t)t * rows_total + h * N + row) * NE + e] = d;
+                    }
                     vals[h][s][t] = pass_pairs8(kact, ws_s, (float)d, ws_m, (float)xsv[t]);
                 }
             }
+            // one pass: the row is complete; one lane stores it now, so that
+            // only the last row's fold and store follow the last load
+            if (!ARGMAX && MT == 1 && p.J == 1 && lane == 0)
+                emit_row(slot + p.nslots * s, vals[0][s][0], vals[NH - 1][s][0], dxv[0]);
         }
 #ifdef WQ_TIMELINE
         {
@@ -434,7 +451,9 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
             }
         };
         static_assert(IPW * MT <= 64, "one lane per (row, token)");
-        if (p.J == 1) {
+        if (p.J == 1 && !ARGMAX && MT == 1) {
+            WQ_STAMP(4, 0u);  // every row was stored as it completed
+        } else if (p.J == 1) {
             // lane s * MT + t of the wave emits (token t, its row s)
             float v0 = 0.0f, v1 = 0.0f, dsel = 0.0f;
             int tsel = -1, rsel = 0;
