@@ -76,10 +76,12 @@ constexpr unsigned kArgmaxSpinLimit = 1u << 22;
 //     at the same coherence point.
 // The HIP memory model guarantees visibility only through release/acquire
 // pairs, so points 1, 2 and 4 rest on this hardware's completion order rather
-// than on the language model.  The last workgroup adds an agent-scope
-// acquire fence before its loads (one L2 invalidate on one XCD; measured
-// 0.3-0.4 us per call on the lm_head shapes), so no stale line of its XCD's
-// L2 can be read even if a key load were served from the L2.
+// than on the language model.  No acquire fence precedes the key loads: they
+// are agent-scope atomic loads (`global_load ... sc1`, performed at the
+// coherence point, never served from a stale line of the XCD's L2) of words
+// that only agent-scope atomics write, which is what the gfx950 memory model
+// makes coherent without a fence; a fence would only add one L2 invalidate
+// (0.3-0.4 us per call, measured) for the non-atomic loads that follow none.
 //
 // Cost: the combine adds 2.5-4 us per call on the lm_head shapes, almost all
 // of it after the last stream ends (the last tickets landing, the final
@@ -140,7 +142,6 @@ __device__ __forceinline__ void argmax_combine(const ArgmaxArgs& am, int M, int 
         if (tid == 0) timed_out = done ? 0u : 1u;
     }
     __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     // Wave w reduces tokens w, w + nwaves, ...: lane l reads slot l's key
     // (independent device-coherent loads), a 64-lane maximum (exact,
     // order-free), and each lane then clears the key it read.
