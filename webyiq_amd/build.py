@@ -46,12 +46,14 @@ CFLAGS = [
     "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 # Per-source flags: kernel-argument preloading.  The leading arguments of the
-# GEMV (nine, 14 SGPRs), the activation quantisers (four, 6 SGPRs) and the
-# chunk merge (five, 7 SGPRs) are what their first global loads need;
-# preloaded, they arrive in SGPRs with the wave, so no scalar load of the
-# argument segment precedes the first load.  (Kernels whose first argument is
-# a parameter struct preload nothing.)
+# GEMV (nine, 14 SGPRs), the MFMA GEMV of 3..8 tokens (eight, 13 SGPRs), the
+# activation quantisers (four, 6 SGPRs) and the chunk merge (five, 7 SGPRs)
+# are what their first global loads need; preloaded, they arrive in SGPRs
+# with the wave, so no scalar load of the argument segment precedes the
+# first load.  (Kernels whose first argument is a parameter struct preload
+# nothing.)
 SOURCE_FLAGS = {"gemv_q4q8.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
+                "gemv_mfma.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
                 "quant_act.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=4"],
                 "attn_combine.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=5"]}
 # what the host pass prints for the device-only feature above (harmless)

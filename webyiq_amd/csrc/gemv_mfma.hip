@@ -303,19 +303,24 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
 // Store and argmax instances are held to 96 VGPRs: five workgroups per CU
 // (the LDS allows five) overlap one another's loads and compute (38.65
 // against 39.86 us at 8 tokens x 151,936 rows; six spill).
+// The leading arguments are what the first loads need (operand pointers,
+// N, K, M and the group counts packed as NG | NGP << 16); this translation
+// unit preloads them into SGPRs (-amdgpu-kernarg-preload-count=8), so no
+// scalar load of the argument segment precedes the first loads.  The rest is
+// read from the parameter struct once the loads are in flight.
 template <int MT, int MODE, bool ARGMAX>
-__global__ __launch_bounds__(64 * kRowsWaves, (MODE == 0 ? 5 : 1)) void gemv_mfma_rows_kernel(MfmaGemvParams p) {
+__global__ __launch_bounds__(64 * kRowsWaves, (MODE == 0 ? 5 : 1)) void gemv_mfma_rows_kernel(
+    const uint32_t* kwq, const uint32_t* kws, const int8_t* kxq, const int32_t* kxs, const float* kdx, int kN, int kK,
+    uint32_t kmg, MfmaGemvParams pk) {
     constexpr int NH = MODE == 2 ? 2 : 1;
     constexpr int RB = 16 * kRowsWaves;  // rows per workgroup: one 16-row block per wave
     constexpr int NT = 64 * kRowsWaves;  // threads
     extern __shared__ __align__(16) unsigned char smem[];
+    MfmaGemvParams p = pk;
+    p.a.wq = kwq; p.a.ws = kws; p.a.xq = kxq; p.a.xs = kxs; p.a.dx = kdx;
+    p.a.N = kN; p.a.K = kK; p.a.M = kmg & 255;
+    p.NG = (kmg >> 8) & 255; p.NGP = kmg >> 16;
     const LinearArgs& a = p.a;
-    pin_arg(a.wq); pin_arg(a.ws); pin_arg(a.xq); pin_arg(a.dx); pin_arg(a.xs); pin_arg(a.y);
-    pin_arg(a.acc_dump); pin_arg(a.N); pin_arg(a.K); pin_arg(a.M); pin_arg(p.NG); pin_arg(p.NGP);
-    if (ARGMAX) {
-        pin_arg(p.am.ids); pin_arg(p.am.tok_out); pin_arg(p.am.keys); pin_arg(p.am.ticket);
-        pin_arg(p.nblocks);
-    }
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = (int)a.K;
     const int NG = p.NG, NGP = p.NGP;  // NG <= kMaxGpw
@@ -364,6 +369,12 @@ __global__ __launch_bounds__(64 * kRowsWaves, (MODE == 0 ? 5 : 1)) void gemv_mfm
             for (int h = 0; h < NH; ++h)  // plain loads, as in gemv_mfma_kernel
                 wv[h][i] = load16(reinterpret_cast<const unsigned char*>(a.wq) + (row + h * N) * (K / 2) +
                                   64 * gi + 16 * q);
+        }
+        // the rest of the arguments, in SGPRs now that the loads are in flight
+        pin_arg(a.y); pin_arg(a.acc_dump);
+        if (ARGMAX) {
+            pin_arg(p.am.ids); pin_arg(p.am.tok_out); pin_arg(p.am.keys); pin_arg(p.am.ticket);
+            pin_arg(p.nblocks);
         }
         // the direct-to-LDS loads and the scale words (issued first) have
         // landed: at most the weight loads remain in flight
@@ -517,15 +528,21 @@ hipError_t launch_gemv_mfma(const LinearArgs& a, const ArgmaxArgs* am, hipStream
         const unsigned rgrid = (unsigned)((a.N + rbr - 1) / rbr);
         gp.nblocks = (int)rgrid;
         dim3 g(rgrid), b(64 * kRowsWaves);
+        // the preloaded arguments: M, NG and NGP packed in one word
+        const uint32_t mg = (uint32_t)a.M | ((uint32_t)gp.NG << 8) | ((uint32_t)gp.NGP << 16);
+#define WQ_ROWS_LAUNCH(MODE_, ARGMAX_)                                                                          \
+    hipLaunchKernelGGL((gemv_mfma_rows_kernel<8, MODE_, ARGMAX_>), g, b, lds_rows, s, a.wq, a.ws, a.xq, a.xs, \
+                       a.dx, (int)a.N, (int)a.K, mg, gp)
         if (am) {
-            hipLaunchKernelGGL((gemv_mfma_rows_kernel<8, 0, true>), g, b, lds_rows, s, gp);
+            WQ_ROWS_LAUNCH(0, true);
         } else {
             switch (a.mode) {
-                case 0: hipLaunchKernelGGL((gemv_mfma_rows_kernel<8, 0, false>), g, b, lds_rows, s, gp); break;
-                case 1: hipLaunchKernelGGL((gemv_mfma_rows_kernel<8, 1, false>), g, b, lds_rows, s, gp); break;
-                default: hipLaunchKernelGGL((gemv_mfma_rows_kernel<8, 2, false>), g, b, lds_rows, s, gp); break;
+                case 0: WQ_ROWS_LAUNCH(0, false); break;
+                case 1: WQ_ROWS_LAUNCH(1, false); break;
+                default: WQ_ROWS_LAUNCH(2, false); break;
             }
         }
+#undef WQ_ROWS_LAUNCH
         return hipGetLastError();
     }
     if (am) return launch_rbw<8, 0, true>(gp, rbw, lds, grid, s);
