@@ -1,4 +1,8 @@
-"""The packed-fp32 guard of the HIP build (webyiq_amd/build.py CFLAGS).
+"""Checks of the HIP build's flags on the built library (no GPU needed):
+the packed-fp32 guard, no register spills in the production GEMM and the
+headline GEMV, and kernel-argument preloading on the decode kernels.
+
+The packed-fp32 guard (webyiq_amd/build.py CFLAGS).
 
 The library is compiled with `-Xclang -target-feature -Xclang
 -packed-fp32-ops`.  hipcc's host pass does not know that feature and says
@@ -96,3 +100,50 @@ def test_production_gemm_and_headline_gemv_use_no_scratch(tmp_path):
     assert not {k: v for k, v in gemm.items() if v}, "spilling GEMM instances"
     head = [k for k in scratch if "gemv_kernelILi1ELi0ELi128ELb1ELi2ELb0ELb0E" in k]
     assert head and all(scratch[k] == 0 for k in head)
+
+
+def kernel_bodies(tmp_path):
+    """{mangled kernel name: [instruction mnemonics with operands]} of the
+    built library's gfx950 code objects."""
+    lib = tmp_path / "lib.so"
+    shutil.copy(hipbuild.LIB, lib)
+    subprocess.run([OBJDUMP, "--offloading", str(lib)], check=True, capture_output=True, cwd=tmp_path)
+    bodies, name = {}, None
+    for o in sorted(p for p in tmp_path.iterdir() if "amdgcn" in p.name and "gfx950" in p.name):
+        asm = subprocess.run([OBJDUMP, "-d", "--mcpu=gfx950", "--no-show-raw-insn", str(o)], check=True,
+                             capture_output=True, text=True).stdout
+        for line in asm.splitlines():
+            m = re.match(r"^[0-9a-f]+ <(\S+)>:$", line)
+            if m:
+                name = m.group(1)
+                bodies[name] = []
+            elif name and line.startswith("\t"):
+                bodies[name].append(line.split("//")[0].strip())
+    return bodies
+
+
+@pytest.mark.skipif(not (os.path.exists(hipbuild.LIB) and os.path.exists(OBJDUMP)),
+                    reason="library not built or llvm-objdump missing")
+def test_decode_kernels_issue_their_first_load_without_an_argument_wait(tmp_path):
+    """The decode-path kernels take the arguments their first loads need as
+    leading arguments preloaded into SGPRs (build.py SOURCE_FLAGS): their
+    code starts with the preload's compatibility preamble (scalar loads of
+    those arguments, a wait and a branch over padding, run only where the
+    firmware does not preload), and after it the first global load comes
+    before any wait for a scalar load (one merely issued is no stall)."""
+    bodies = kernel_bodies(tmp_path)
+    wanted = ["gemv_kernelILi1ELi0ELi128ELb1ELi2ELb0ELb0E",   # the headline GEMV
+              "gemv_kernelILi1ELi2ELi128ELb1ELi3ELb0ELb1E",   # fused norm + quant + gate_up
+              "quant_split_kernelILb1ELb1ELi128ELi8E",        # norm + quantiser
+              "attn_combine_kernelILi2E",                     # chunk merge
+              "gemv_mfma_rows_kernelILi8ELi0ELb1E"]           # lm_head at 3..8 tokens
+    for w in wanted:
+        names = [n for n in bodies if w in n]
+        assert names, f"{w}: kernel not found"
+        ins = bodies[names[0]]
+        br = next(i for i, s in enumerate(ins) if s.startswith("s_branch"))
+        assert all(s.startswith(("s_load", "s_waitcnt")) for s in ins[:br]), f"{w}: no preload preamble"
+        body = [s for s in ins[br + 1:] if not s.startswith("s_nop")]
+        first = next(i for i, s in enumerate(body) if s.startswith("global_load"))
+        early = [s for s in body[:first] if "s_waitcnt" in s and "lgkmcnt" in s]
+        assert not early, f"{w}: a wait for argument loads before the first global load: {early}"

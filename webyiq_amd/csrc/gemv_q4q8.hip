@@ -8,9 +8,9 @@
 // MI355X mapping.  The packed weight matrix is one HBM stream.  A wavefront
 // pass reads 1 KiB of one row (64 lanes x 16 B: one fully coalesced
 // global_load_dwordx4), i.e. 2048 codes; a row of K codes takes J = K/2048
-// passes.  Wave w of a workgroup serves pass j = w % J for rows
-// slot, slot + nslots, ... (slot = w / J), so each lane keeps the 32
-// activations of its pass in registers for every token.  All weight loads of
+// passes.  Wave w of a workgroup serves pass j = w / nslots for rows
+// slot, slot + nslots, ... (slot = w % nslots; nslots is 1, 2 or 4), so each
+// lane keeps the 32 activations of its pass in registers for every token.  All weight loads of
 // a workgroup are issued before the first one is consumed (IPW rows per wave),
 // so the whole matrix is in flight at once across the chip.
 //
