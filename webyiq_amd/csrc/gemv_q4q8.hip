@@ -52,8 +52,15 @@ __device__ unsigned long long wq_timeline[kTimelineWgs * 8];
         if (!QIN && !ARGMAX && MT == 1 && threadIdx.x == 0 && blockIdx.x < kTimelineWgs)              \
             wq_timeline[blockIdx.x * 8 + (k)] = __builtin_amdgcn_s_memrealtime() + ((dep) == 0x7654321u); \
     } while (0)
+// the same stamps from gemv_one_kernel (one token by construction)
+#define WQ_STAMP_ONE(k, dep)                                                                          \
+    do {                                                                                              \
+        if (threadIdx.x == 0 && blockIdx.x < kTimelineWgs)                                            \
+            wq_timeline[blockIdx.x * 8 + (k)] = __builtin_amdgcn_s_memrealtime() + ((dep) == 0x7654321u); \
+    } while (0)
 #else
 #define WQ_STAMP(k, dep) ((void)0)
+#define WQ_STAMP_ONE(k, dep) ((void)0)
 #endif
 
 namespace {
@@ -745,6 +752,72 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
     }
 }
 
+// One token, one 2048-code pass per row (K = 2048), per-token activations
+// at group 128: the decode GEMV's most common instance (the headline shape,
+// the qkv and gate_up projections of a hidden size of 2048), in a kernel of
+// its own.  The arithmetic and its order are gemv_kernel's one-token
+// register epilogue exactly (dot32, quad_sum, pass_pairs8, times dx), so
+// outputs are bit-identical to it; what this kernel drops is the
+// generality around them (plan fields decoded at run time, partial passes,
+// the pass-count and debug-dump branches), which costs each wave
+// instructions before its last load is issued.  Four waves per workgroup,
+// one row slot each, IPW rows per wave; rows past N re-read row N - 1 and
+// store nothing.  The seven arguments are preloaded into SGPRs (13 of them).
+constexpr int kOneSlots = 4;
+
+template <int MODE, int IPW>
+__global__ __launch_bounds__(64 * kOneSlots) void gemv_one_kernel(const uint32_t* wq, const int8_t* xq,
+                                                                   const uint32_t* ws, const int32_t* xs,
+                                                                   const float* dx, float* y, int N) {
+    constexpr int NH = MODE == 2 ? 2 : 1;  // gate (+ up) row halves
+    constexpr uint32_t kRowBytes = kGemvPassK / 2, kGroups = kGemvPassK / 128;
+    WQ_STAMP_ONE(0, 0u);
+    const int lane = threadIdx.x & 63;
+    const int slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r0 = (int)blockIdx.x * (kOneSlots * IPW);
+    const uint32_t kpos = 32u * lane;  // this lane's 32 codes
+    const uint32_t g = (uint32_t)lane >> 2;  // its group of 128
+    // the activations first (L2-resident), then every row's weights and scale word
+    const uint4 xa = load16(xq + kpos), xb = load16(xq + kpos + 16);
+    const int32_t xsv = xs[g];
+    const float dxv = dx[0];
+    asm volatile("" ::: "memory");
+    uint4 wv[NH][IPW];
+    uint32_t sv[NH][IPW];
+#pragma unroll
+    for (int s = 0; s < IPW; ++s) {
+        const int row = min(r0 + slot + kOneSlots * s, N - 1);
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            const size_t rh = (size_t)(row + h * N);
+            wv[h][s] = load_stream16(reinterpret_cast<const unsigned char*>(wq) + rh * kRowBytes + kpos / 2);
+            sv[h][s] = ws[rh * kGroups + g];
+        }
+        asm volatile("" ::: "memory");  // loads stay in row order: row s lands before row s + 1
+    }
+    WQ_STAMP_ONE(1, xa.x ^ xb.w ^ (uint32_t)xsv ^ __float_as_uint(dxv));
+    WQ_STAMP_ONE(2, wv[0][0].x ^ sv[0][0]);
+#pragma unroll
+    for (int s = 0; s < IPW; ++s) {
+        float v[NH];
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            const int d = quad_sum(dot32(wv[h][s], xa, xb));
+            v[h] = pass_pairs8(true, f16lo(sv[h][s]), (float)d, f16hi(sv[h][s]), (float)xsv);
+        }
+        const int row = r0 + slot + kOneSlots * s;
+        if (lane == 0 && row < N) {  // the row is complete: stored now
+            float* yo = y + row;
+            const float o = v[0] * dxv;
+            if (MODE == 0) *yo = o;
+            else if (MODE == 1) *yo = *yo + o;
+            else *yo = silu_mul(o, v[NH - 1] * dxv);
+        }
+        if (s == IPW - 1) WQ_STAMP_ONE(3, __float_as_uint(v[0]));
+    }
+    WQ_STAMP_ONE(4, 0u);
+}
+
 // ------------------------------------------------------------ dispatch ----
 
 struct Plan {
@@ -889,9 +962,35 @@ GemvParams params_of(const LinearArgs& a, const Plan& pl) {
 
 }  // namespace
 
+template <int MODE>
+hipError_t launch_one(const LinearArgs& a, int ipw, unsigned grid, hipStream_t s) {
+    dim3 g(grid), b(64 * kOneSlots);
+#define WQ_ONE_LAUNCH(IPW) \
+    hipLaunchKernelGGL((gemv_one_kernel<MODE, IPW>), g, b, 0, s, a.wq, a.xq, a.ws, a.xs, a.dx, a.y, (int)a.N)
+    switch (ipw) {
+        case 1: WQ_ONE_LAUNCH(1); break;
+        case 2: WQ_ONE_LAUNCH(2); break;
+        case 3: WQ_ONE_LAUNCH(3); break;
+        case 4: WQ_ONE_LAUNCH(4); break;
+        case 6: WQ_ONE_LAUNCH(6); break;
+        default: WQ_ONE_LAUNCH(8); break;
+    }
+#undef WQ_ONE_LAUNCH
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv(const LinearArgs& a, hipStream_t s) {
     if (gemv_mfma_fits(a)) return launch_gemv_mfma(a, nullptr, s);
     Plan pl = make_plan(a, false);
+    // one token, one full pass, per-token group 128, no debug dump: the
+    // specialised kernel on the same plan (bit-identical outputs)
+    if (a.M == 1 && a.GA == a.K && a.G == 128 && a.K == kGemvPassK && !a.acc_dump) {
+        switch (a.mode) {
+            case 0: return launch_one<0>(a, pl.IPW, pl.grid, s);
+            case 1: return launch_one<1>(a, pl.IPW, pl.grid, s);
+            default: return launch_one<2>(a, pl.IPW, pl.grid, s);
+        }
+    }
     GemvParams gp = params_of(a, pl);
     switch (a.mode) {
         case 0: return launch_mt<0, false, false>(pl, gp, s);
