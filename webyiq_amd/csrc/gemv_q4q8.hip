@@ -763,6 +763,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
 // instructions before its last load is issued.  Four waves per workgroup,
 // one row slot each, IPW rows per wave; rows past N re-read row N - 1 and
 // store nothing.  The seven arguments are preloaded into SGPRs (13 of them).
+// (The grid has its own rows-per-wave rule, at the dispatch.)
 constexpr int kOneSlots = 4;
 
 template <int MODE, int IPW>
@@ -981,16 +982,25 @@ hipError_t launch_one(const LinearArgs& a, int ipw, unsigned grid, hipStream_t s
 
 hipError_t launch_gemv(const LinearArgs& a, hipStream_t s) {
     if (gemv_mfma_fits(a)) return launch_gemv_mfma(a, nullptr, s);
-    Plan pl = make_plan(a, false);
     // one token, one full pass, per-token group 128, no debug dump: the
-    // specialised kernel on the same plan (bit-identical outputs)
+    // specialised kernel (bit-identical outputs; the rows per wave do not
+    // change any output, only which wave computes a row)
     if (a.M == 1 && a.GA == a.K && a.G == 128 && a.K == kGemvPassK && !a.acc_dump) {
+        // the fewest rows per wave that keep the grid within the target, one
+        // included (measured: one row per wave at N = 2048 and 3072, 2.19
+        // and 2.33 us against 2.24 and 2.42 with two; two at N = 6144)
+        int ipw = 8;
+        for (int c : {1, 2, 3, 4, 6, 8}) {
+            if ((a.N + kOneSlots * c - 1) / (kOneSlots * c) <= kGemvTargetWgs) { ipw = c; break; }
+        }
+        const unsigned grid = (unsigned)((a.N + kOneSlots * ipw - 1) / (kOneSlots * ipw));
         switch (a.mode) {
-            case 0: return launch_one<0>(a, pl.IPW, pl.grid, s);
-            case 1: return launch_one<1>(a, pl.IPW, pl.grid, s);
-            default: return launch_one<2>(a, pl.IPW, pl.grid, s);
+            case 0: return launch_one<0>(a, ipw, grid, s);
+            case 1: return launch_one<1>(a, ipw, grid, s);
+            default: return launch_one<2>(a, ipw, grid, s);
         }
     }
+    Plan pl = make_plan(a, false);
     GemvParams gp = params_of(a, pl);
     switch (a.mode) {
         case 0: return launch_mt<0, false, false>(pl, gp, s);
