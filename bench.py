@@ -12,7 +12,11 @@ with --launch graph, captured as two HIP graphs) on one stream behind a gate
 of --settle untimed launches of the same GEMV replayed as a graph, so the
 GPU runs them back to back with no host submission gap and at the clocks of
 back-to-back decode launches (class Gate); HIP events on that stream around
-the K launches time the region, which is synchronised on both sides.
+the K launches time the region, which is synchronised on both sides.  The
+events are created with hipEventDisableSystemFence (class TimingEvents: the
+flag hip_runtime_api.h gives for events that only measure time), so
+recording them adds no cache writeback and invalidate to the region;
+--torch-events times with torch's default events instead.
 
 Printed JSON line:
   value       whole-job GEMV throughput, algorithmic GB/s over the K steps
@@ -77,6 +81,9 @@ def parse():
     ap.add_argument("--settle", type=int, default=1000,
                     help="untimed GEMV launches (other weight copies), replayed as a graph ahead of "
                          "the warm-up: the gate that covers the host's enqueue and settles the clocks")
+    ap.add_argument("--torch-events", action="store_true",
+                    help="time with torch's default events (a system-scope fence at each record) "
+                         "instead of HIP events created with hipEventDisableSystemFence")
     ap.add_argument("--no-kernel-clock", action="store_true",
                     help="skip the device-clock duration of single launches (roofline.kernel_us)")
     ap.add_argument("--timeline", action="store_true",
@@ -106,6 +113,80 @@ class Launcher:
             raise RuntimeError(f"launch failed [{rc}]")
 
 
+class TimingEvents:
+    """Two timing events (start, end) for one timed region.
+
+    By default they are created on the HIP runtime that torch loaded with
+    hipEventDisableSystemFence: the flag hip_runtime_api.h gives for events
+    used only to measure time.  A default event performs a system-scope
+    fence when it is recorded (a cache writeback and invalidate); its cost
+    then lands in the timed region although it belongs to the event, not to
+    the launches between the two events (measured at the driver's 20
+    launches: 2.96-2.99 us per launch with these events, 3.04-3.19 with
+    torch's default ones, alternating on one box).  --torch-events (or a
+    torch build without that runtime file) uses torch's default events.
+    Either way the region holds the same launches on the same stream, and
+    the caller synchronises on both sides."""
+    FLAGS = 0x20000000  # hipEventDisableSystemFence
+    hip = None
+    kind = "torch"
+
+    @classmethod
+    def configure(cls, torch, use_torch=False):
+        cls.kind = "torch"
+        if use_torch:
+            return
+        path = os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so")
+        if not os.path.exists(path):
+            return
+        h = ctypes.CDLL(path)  # the runtime torch already loaded: the same file, the same handle
+        h.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        for f in ("hipEventCreateWithFlags", "hipEventRecord", "hipEventElapsedTime", "hipEventDestroy"):
+            getattr(h, f).restype = ctypes.c_int
+        cls.hip = h
+        cls.kind = "hip_no_system_fence"
+
+    def __init__(self, torch):
+        self.native = self.kind != "torch"
+        if not self.native:
+            self.ev = [torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
+            return
+        self.ev = []
+        for _ in range(2):
+            e = ctypes.c_void_p()
+            rc = self.hip.hipEventCreateWithFlags(ctypes.byref(e), self.FLAGS)
+            if rc:
+                raise RuntimeError(f"hipEventCreateWithFlags failed [{rc}]")
+            self.ev.append(e)
+
+    def record(self, i, stream):
+        """Record event i (0 = start, 1 = end) on `stream`, a torch stream."""
+        if not self.native:
+            self.ev[i].record(stream)
+            return
+        rc = self.hip.hipEventRecord(self.ev[i], ctypes.c_void_p(stream.cuda_stream))
+        if rc:
+            raise RuntimeError(f"hipEventRecord failed [{rc}]")
+
+    def seconds(self):
+        """Start-to-end time in seconds (the caller has synchronised)."""
+        if not self.native:
+            return self.ev[0].elapsed_time(self.ev[1]) * 1e-3
+        ms = ctypes.c_float()
+        rc = self.hip.hipEventElapsedTime(ctypes.byref(ms), self.ev[0], self.ev[1])
+        if rc:
+            raise RuntimeError(f"hipEventElapsedTime failed [{rc}]")
+        return ms.value * 1e-3
+
+    def __del__(self):
+        if getattr(self, "native", False):
+            for e in self.ev:
+                self.hip.hipEventDestroy(e)
+
+
 def graph_time(torch, launches, reps):
     """Mean time per launch of `launches` captured in one HIP graph and
     replayed `reps` times back to back (seconds)."""
@@ -123,15 +204,15 @@ def graph_time(torch, launches, reps):
             ln(cs)
     g.replay()
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    ev = TimingEvents(torch)
     torch.cuda.synchronize()
-    e0.record()
+    cur = torch.cuda.current_stream()
+    ev.record(0, cur)
     for _ in range(reps):
         g.replay()
-    e1.record()
+    ev.record(1, cur)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e-3 / (reps * len(launches))
+    return ev.seconds() / (reps * len(launches))
 
 
 class Gate:
@@ -186,7 +267,7 @@ class Gate:
         for _ in range(6):
             torch.cuda.synchronize()
             eg = torch.cuda.Event()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev = TimingEvents(torch)
             with torch.cuda.stream(s):
                 for _ in range(self.passes):
                     if self.gs is not None:
@@ -200,20 +281,20 @@ class Gate:
                 elif not graph:
                     for ln in warm:
                         ln(cs)
-                e0.record(s)
+                ev.record(0, s)
                 if gt is not None:
                     gt.replay()
                 else:
                     for ln in seq:
                         ln(cs)
-                e1.record(s)
+                ev.record(1, s)
             covered = not eg.query()  # the gate still ran when the host was done
             torch.cuda.synchronize()
             if covered:
                 break
             self.passes *= 2
         self.covered = covered
-        return e0.elapsed_time(e1) * 1e-3 / len(seq)
+        return ev.seconds() / len(seq)
 
 
 def main():
@@ -225,6 +306,7 @@ def main():
     import torch
     from webyiq_amd import _lib, ops
 
+    TimingEvents.configure(torch, use_torch=args.torch_events)
     lib = _lib.load()
     sys.path.insert(0, HERE)
     from oracle import oracle as orc
@@ -300,6 +382,7 @@ def main():
                    "bytes_per_launch": nbytes, "parallelism": "single GPU"},
         "gemv_us_per_launch": round(t_launch * 1e6, 3),
         "launch": args.launch,
+        "timing_events": TimingEvents.kind,
         "gate_covered_host_enqueue": gate_covered,
         "settle_launches": args.settle * gate.passes,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
