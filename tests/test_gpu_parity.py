@@ -439,11 +439,14 @@ def test_gemm_group32_wide_widths(M, mode, stride):
 
 @pytest.mark.parametrize("K,N", [(2048, 6144), (6144, 2048)])
 def test_gemm_prefill_production_int32(K, N):
-    """BASELINE configs[3] on the production kernel (the tile width the
-    launcher picks for M = 1024, not a debug instance): the int32 group sums
-    of all 1,024 tokens bit-exact against an exact integer reference (one
-    float64 product per group, exact for these magnitudes), and the fp32
-    output of all 1,024 tokens within rel 1e-5 of the oracle."""
+    """BASELINE configs[3] at the production tile width (the one the
+    launcher picks for M = 1024): the int32 group sums of all 1,024 tokens
+    bit-exact against an exact integer reference (one float64 product per
+    group, exact for these magnitudes), and the fp32 output of all 1,024
+    tokens within rel 1e-5 of the oracle.  The sums come from the dump
+    hook, a sibling instance of the same template (DUMP set); its fp32
+    output is checked bit-identical to the production instance's below,
+    which ties the sums to the production kernel."""
     M, G = 1024, 128
     note(f"gemm production int32 M={M} K={K} N={N}")
     wq, ws, x, xq, dx, xs = setup_linear(K * 3 + N, M, K, N, G, None)
@@ -461,7 +464,7 @@ def test_gemm_prefill_production_int32(K, N):
     got = host(y)
     want = oracle_linear_tokens(wq, ws, K, G, xq, dx, xs)
     assert rel_err(got, want) < 1e-5
-    # the plain entry point runs the same kernel and gives the same bits
+    # the production instance (plain entry point) gives the same bits
     y2 = host(ops.gemm(w, a))
     assert np.array_equal(y2.view(np.uint32), got.view(np.uint32))
 
