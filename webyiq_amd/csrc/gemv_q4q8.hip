@@ -752,24 +752,27 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
     }
 }
 
-// One token, one 2048-code pass per row (K = 2048), per-token activations
-// at group 128: the decode GEMV's most common instance (the headline shape,
-// the qkv and gate_up projections of a hidden size of 2048), in a kernel of
-// its own.  The arithmetic and its order are gemv_kernel's one-token
-// register epilogue exactly (dot32, quad_sum, pass_pairs8, times dx), so
-// outputs are bit-identical to it; what this kernel drops is the
-// generality around them (plan fields decoded at run time, partial passes,
-// the pass-count and debug-dump branches), which costs each wave
-// instructions before its last load is issued.  Four waves per workgroup,
-// one row slot each, IPW rows per wave; rows past N re-read row N - 1 and
-// store nothing.  The seven arguments are preloaded into SGPRs (13 of them).
-// (The grid has its own rows-per-wave rule, at the dispatch.)
+// One or two tokens (MT), one 2048-code pass per row (K = 2048), per-token
+// activations at group 128: the decode GEMV's most common instances (the
+// headline shape, the qkv and gate_up projections of a hidden size of 2048,
+// and their two-token verify launches), in a kernel of their own.  The
+// arithmetic and its order are gemv_kernel's register epilogue exactly
+// (dot32, quad_sum, pass_pairs8, times dx, per token), which its LDS
+// epilogue for several tokens reproduces, so outputs are bit-identical to
+// either; what this kernel drops is the generality around them (plan
+// fields decoded at run time, partial passes, the pass-count and
+// debug-dump branches, and for two tokens the group sums' LDS round trip
+// and barrier).  Four waves per workgroup, one row slot each, IPW rows per
+// wave; rows past N re-read row N - 1 and store nothing.  The seven
+// arguments are preloaded into SGPRs (13 of them).  (The grid has its own
+// rows-per-wave rule, at the dispatch.)
 constexpr int kOneSlots = 4;
 
-template <int MODE, int IPW>
+template <int MODE, int IPW, int MT>
 __global__ __launch_bounds__(64 * kOneSlots) void gemv_one_kernel(const uint32_t* wq, const int8_t* xq,
                                                                    const uint32_t* ws, const int32_t* xs,
                                                                    const float* dx, float* y, int N) {
+    static_assert(MT == 1 || MT == 2, "one or two tokens");
     constexpr int NH = MODE == 2 ? 2 : 1;  // gate (+ up) row halves
     constexpr uint32_t kRowBytes = kGemvPassK / 2, kGroups = kGemvPassK / 128;
     WQ_STAMP_ONE(0, 0u);
@@ -779,9 +782,16 @@ __global__ __launch_bounds__(64 * kOneSlots) void gemv_one_kernel(const uint32_t
     const uint32_t kpos = 32u * lane;  // this lane's 32 codes
     const uint32_t g = (uint32_t)lane >> 2;  // its group of 128
     // the activations first (L2-resident), then every row's weights and scale word
-    const uint4 xa = load16(xq + kpos), xb = load16(xq + kpos + 16);
-    const int32_t xsv = xs[g];
-    const float dxv = dx[0];
+    uint4 xa[MT], xb[MT];
+    int32_t xsv[MT];
+    float dxv[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        xa[t] = load16(xq + t * kGemvPassK + kpos);
+        xb[t] = load16(xq + t * kGemvPassK + kpos + 16);
+        xsv[t] = xs[t * (int)kGroups + g];
+        dxv[t] = dx[t];
+    }
     asm volatile("" ::: "memory");
     uint4 wv[NH][IPW];
     uint32_t sv[NH][IPW];
@@ -796,25 +806,30 @@ __global__ __launch_bounds__(64 * kOneSlots) void gemv_one_kernel(const uint32_t
         }
         asm volatile("" ::: "memory");  // loads stay in row order: row s lands before row s + 1
     }
-    WQ_STAMP_ONE(1, xa.x ^ xb.w ^ (uint32_t)xsv ^ __float_as_uint(dxv));
+    WQ_STAMP_ONE(1, xa[0].x ^ xb[0].w ^ (uint32_t)xsv[0] ^ __float_as_uint(dxv[0]));
     WQ_STAMP_ONE(2, wv[0][0].x ^ sv[0][0]);
 #pragma unroll
     for (int s = 0; s < IPW; ++s) {
-        float v[NH];
+        float v[MT][NH];
 #pragma unroll
-        for (int h = 0; h < NH; ++h) {
-            const int d = quad_sum(dot32(wv[h][s], xa, xb));
-            v[h] = pass_pairs8(true, f16lo(sv[h][s]), (float)d, f16hi(sv[h][s]), (float)xsv);
-        }
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const int d = quad_sum(dot32(wv[h][s], xa[t], xb[t]));
+                v[t][h] = pass_pairs8(true, f16lo(sv[h][s]), (float)d, f16hi(sv[h][s]), (float)xsv[t]);
+            }
         const int row = r0 + slot + kOneSlots * s;
         if (lane == 0 && row < N) {  // the row is complete: stored now
-            float* yo = y + row;
-            const float o = v[0] * dxv;
-            if (MODE == 0) *yo = o;
-            else if (MODE == 1) *yo = *yo + o;
-            else *yo = silu_mul(o, v[NH - 1] * dxv);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                float* yo = y + (size_t)t * N + row;
+                const float o = v[t][0] * dxv[t];
+                if (MODE == 0) *yo = o;
+                else if (MODE == 1) *yo = *yo + o;
+                else *yo = silu_mul(o, v[t][NH - 1] * dxv[t]);
+            }
         }
-        if (s == IPW - 1) WQ_STAMP_ONE(3, __float_as_uint(v[0]));
+        if (s == IPW - 1) WQ_STAMP_ONE(3, __float_as_uint(v[0][0]));
     }
     WQ_STAMP_ONE(4, 0u);
 }
@@ -963,11 +978,11 @@ GemvParams params_of(const LinearArgs& a, const Plan& pl) {
 
 }  // namespace
 
-template <int MODE>
+template <int MODE, int MT>
 hipError_t launch_one(const LinearArgs& a, int ipw, unsigned grid, hipStream_t s) {
     dim3 g(grid), b(64 * kOneSlots);
 #define WQ_ONE_LAUNCH(IPW) \
-    hipLaunchKernelGGL((gemv_one_kernel<MODE, IPW>), g, b, 0, s, a.wq, a.xq, a.ws, a.xs, a.dx, a.y, (int)a.N)
+    hipLaunchKernelGGL((gemv_one_kernel<MODE, IPW, MT>), g, b, 0, s, a.wq, a.xq, a.ws, a.xs, a.dx, a.y, (int)a.N)
     switch (ipw) {
         case 1: WQ_ONE_LAUNCH(1); break;
         case 2: WQ_ONE_LAUNCH(2); break;
@@ -982,10 +997,10 @@ hipError_t launch_one(const LinearArgs& a, int ipw, unsigned grid, hipStream_t s
 
 hipError_t launch_gemv(const LinearArgs& a, hipStream_t s) {
     if (gemv_mfma_fits(a)) return launch_gemv_mfma(a, nullptr, s);
-    // one token, one full pass, per-token group 128, no debug dump: the
-    // specialised kernel (bit-identical outputs; the rows per wave do not
-    // change any output, only which wave computes a row)
-    if (a.M == 1 && a.GA == a.K && a.G == 128 && a.K == kGemvPassK && !a.acc_dump) {
+    // one or two tokens, one full pass, per-token group 128, no debug dump:
+    // the specialised kernel (bit-identical outputs; the rows per wave do
+    // not change any output, only which wave computes a row)
+    if (a.M <= 2 && a.GA == a.K && a.G == 128 && a.K == kGemvPassK && !a.acc_dump) {
         // the fewest rows per wave that keep the grid within the target, one
         // included (measured: one row per wave at N = 2048 and 3072, 2.19
         // and 2.33 us against 2.24 and 2.42 with two; two at N = 6144)
@@ -994,10 +1009,17 @@ hipError_t launch_gemv(const LinearArgs& a, hipStream_t s) {
             if ((a.N + kOneSlots * c - 1) / (kOneSlots * c) <= kGemvTargetWgs) { ipw = c; break; }
         }
         const unsigned grid = (unsigned)((a.N + kOneSlots * ipw - 1) / (kOneSlots * ipw));
+        if (a.M == 2) {
+            switch (a.mode) {
+                case 0: return launch_one<0, 2>(a, ipw, grid, s);
+                case 1: return launch_one<1, 2>(a, ipw, grid, s);
+                default: return launch_one<2, 2>(a, ipw, grid, s);
+            }
+        }
         switch (a.mode) {
-            case 0: return launch_one<0>(a, ipw, grid, s);
-            case 1: return launch_one<1>(a, ipw, grid, s);
-            default: return launch_one<2>(a, ipw, grid, s);
+            case 0: return launch_one<0, 1>(a, ipw, grid, s);
+            case 1: return launch_one<1, 1>(a, ipw, grid, s);
+            default: return launch_one<2, 1>(a, ipw, grid, s);
         }
     }
     Plan pl = make_plan(a, false);
