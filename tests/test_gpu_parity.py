@@ -186,6 +186,15 @@ GEMV_CASES = [
     # at the decode-layer shape, 1 and 8 tokens
     (1, 2048, 2048, 128, 32, 1),
     (8, 2048, 2048, 128, 32, 1),
+    # the specialised one-pass kernel at 2..8 tokens (token slots 2, 4, 8;
+    # padding slots re-read the last token and store nothing), within its
+    # rule of at most eight folds per wave, ragged N included
+    (2, 2048, 6144, 128, None, 1),
+    (2, 2048, 6144, 128, None, 2),
+    (4, 2048, 6144, 128, None, 0),   # two rows per wave
+    (5, 2048, 2048, 128, None, 1),
+    (6, 2048, 512, 128, None, 0),
+    (7, 2048, 3000, 128, None, 0),
 ]
 
 

@@ -752,27 +752,30 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint32_t* kwq, const in
     }
 }
 
-// One or two tokens (MT), one 2048-code pass per row (K = 2048), per-token
-// activations at group 128: the decode GEMV's most common instances (the
-// headline shape, the qkv and gate_up projections of a hidden size of 2048,
-// and their two-token verify launches), in a kernel of their own.  The
-// arithmetic and its order are gemv_kernel's register epilogue exactly
-// (dot32, quad_sum, pass_pairs8, times dx, per token), which its LDS
-// epilogue for several tokens reproduces, so outputs are bit-identical to
-// either; what this kernel drops is the generality around them (plan
-// fields decoded at run time, partial passes, the pass-count and
-// debug-dump branches, and for two tokens the group sums' LDS round trip
-// and barrier).  Four waves per workgroup, one row slot each, IPW rows per
-// wave; rows past N re-read row N - 1 and store nothing.  The seven
-// arguments are preloaded into SGPRs (13 of them).  (The grid has its own
+// Up to eight tokens (MT = 1, 2, 4, 8 slots; M of them real), one
+// 2048-code pass per row (K = 2048), per-token activations at group 128:
+// the decode GEMV's most common instances (the headline shape, the qkv and
+// gate_up projections of a hidden size of 2048, and their verify launches),
+// in a kernel of their own.  The arithmetic and its order are gemv_kernel's
+// register epilogue exactly (dot32, quad_sum, pass_pairs8, times dx, per
+// token), which its LDS epilogue for several tokens reproduces, so outputs
+// are bit-identical to either; what this kernel drops is the generality
+// around them (plan fields decoded at run time, partial passes, the
+// pass-count and debug-dump branches, and for several tokens the group
+// sums' LDS round trip and barrier).  Each (token, row) value is folded by
+// the whole wave, so the dispatch takes this kernel only while a wave folds
+// at most eight of them (one_fits).  Four waves per workgroup, one row slot
+// each, IPW rows per wave; rows past N re-read row N - 1 and store nothing;
+// token slots past M re-read token M - 1 and store nothing.  The eight
+// arguments are preloaded into SGPRs (14 of them).  (The grid has its own
 // rows-per-wave rule, at the dispatch.)
 constexpr int kOneSlots = 4;
 
 template <int MODE, int IPW, int MT>
 __global__ __launch_bounds__(64 * kOneSlots) void gemv_one_kernel(const uint32_t* wq, const int8_t* xq,
                                                                    const uint32_t* ws, const int32_t* xs,
-                                                                   const float* dx, float* y, int N) {
-    static_assert(MT == 1 || MT == 2, "one or two tokens");
+                                                                   const float* dx, float* y, int N, int M) {
+    static_assert(MT == 1 || MT == 2 || MT == 4 || MT == 8, "up to eight tokens");
     constexpr int NH = MODE == 2 ? 2 : 1;  // gate (+ up) row halves
     constexpr uint32_t kRowBytes = kGemvPassK / 2, kGroups = kGemvPassK / 128;
     WQ_STAMP_ONE(0, 0u);
@@ -787,10 +790,11 @@ __global__ __launch_bounds__(64 * kOneSlots) void gemv_one_kernel(const uint32_t
     float dxv[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-        xa[t] = load16(xq + t * kGemvPassK + kpos);
-        xb[t] = load16(xq + t * kGemvPassK + kpos + 16);
-        xsv[t] = xs[t * (int)kGroups + g];
-        dxv[t] = dx[t];
+        const int tt = (t == 0 || t < M) ? t : M - 1;  // padding tokens re-read the last one
+        xa[t] = load16(xq + tt * kGemvPassK + kpos);
+        xb[t] = load16(xq + tt * kGemvPassK + kpos + 16);
+        xsv[t] = xs[tt * (int)kGroups + g];
+        dxv[t] = dx[tt];
     }
     asm volatile("" ::: "memory");
     uint4 wv[NH][IPW];
@@ -819,17 +823,24 @@ __global__ __launch_bounds__(64 * kOneSlots) void gemv_one_kernel(const uint32_t
                 v[t][h] = pass_pairs8(true, f16lo(sv[h][s]), (float)d, f16hi(sv[h][s]), (float)xsv[t]);
             }
         const int row = r0 + slot + kOneSlots * s;
-        if (lane == 0 && row < N) {  // the row is complete: stored now
+        // the row is complete: stored now, token t by lane t (its read,
+        // SiLU and store in parallel with the other tokens')
+        float v0 = v[0][0], v1 = v[0][NH - 1], dd = dxv[0];
 #pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                float* yo = y + (size_t)t * N + row;
-                const float o = v[t][0] * dxv[t];
-                if (MODE == 0) *yo = o;
-                else if (MODE == 1) *yo = *yo + o;
-                else *yo = silu_mul(o, v[t][NH - 1] * dxv[t]);
+        for (int t = 1; t < MT; ++t)
+            if (lane == t) {
+                v0 = v[t][0];
+                v1 = v[t][NH - 1];
+                dd = dxv[t];
             }
+        if (lane < MT && lane < M && row < N) {
+            float* yo = y + (size_t)lane * N + row;
+            const float o = v0 * dd;
+            if (MODE == 0) *yo = o;
+            else if (MODE == 1) *yo = *yo + o;
+            else *yo = silu_mul(o, v1 * dd);
         }
-        if (s == IPW - 1) WQ_STAMP_ONE(3, __float_as_uint(v[0][0]));
+        if (s == IPW - 1) WQ_STAMP_ONE(3, __float_as_uint(v0));
     }
     WQ_STAMP_ONE(4, 0u);
 }
@@ -982,7 +993,8 @@ template <int MODE, int MT>
 hipError_t launch_one(const LinearArgs& a, int ipw, unsigned grid, hipStream_t s) {
     dim3 g(grid), b(64 * kOneSlots);
 #define WQ_ONE_LAUNCH(IPW) \
-    hipLaunchKernelGGL((gemv_one_kernel<MODE, IPW, MT>), g, b, 0, s, a.wq, a.xq, a.ws, a.xs, a.dx, a.y, (int)a.N)
+    hipLaunchKernelGGL((gemv_one_kernel<MODE, IPW, MT>), g, b, 0, s, a.wq, a.xq, a.ws, a.xs, a.dx, a.y, (int)a.N, \
+                       (int)a.M)
     switch (ipw) {
         case 1: WQ_ONE_LAUNCH(1); break;
         case 2: WQ_ONE_LAUNCH(2); break;
@@ -995,20 +1007,47 @@ hipError_t launch_one(const LinearArgs& a, int ipw, unsigned grid, hipStream_t s
     return hipGetLastError();
 }
 
+// rows per wave of the specialised kernel: the fewest that keep the grid
+// within the target, one included
+int one_ipw(const LinearArgs& a) {
+    for (int c : {1, 2, 3, 4, 6, 8})
+        if ((a.N + kOneSlots * c - 1) / (kOneSlots * c) <= kGemvTargetWgs) return c;
+    return 8;
+}
+// one or two tokens always; 3..8 while each wave folds at most eight
+// (token, row) values (tokens x row halves x rows per wave), beyond which
+// the LDS epilogue, which spreads the folds over lanes, is faster
+bool one_fits(const LinearArgs& a) {
+    if (a.M <= 2) return true;
+    const int mt = a.M <= 4 ? 4 : 8, nh = a.mode == 2 ? 2 : 1;
+    return mt * nh * one_ipw(a) <= 8;
+}
+
 hipError_t launch_gemv(const LinearArgs& a, hipStream_t s) {
     if (gemv_mfma_fits(a)) return launch_gemv_mfma(a, nullptr, s);
-    // one or two tokens, one full pass, per-token group 128, no debug dump:
-    // the specialised kernel (bit-identical outputs; the rows per wave do
-    // not change any output, only which wave computes a row)
-    if (a.M <= 2 && a.GA == a.K && a.G == 128 && a.K == kGemvPassK && !a.acc_dump) {
+    // up to eight tokens (one_fits), one full pass, per-token group 128, no
+    // debug dump: the specialised kernel (bit-identical outputs; the rows
+    // per wave do not change any output, only which wave computes a row)
+    if (a.M <= 8 && a.GA == a.K && a.G == 128 && a.K == kGemvPassK && !a.acc_dump && one_fits(a)) {
         // the fewest rows per wave that keep the grid within the target, one
         // included (measured: one row per wave at N = 2048 and 3072, 2.19
         // and 2.33 us against 2.24 and 2.42 with two; two at N = 6144)
-        int ipw = 8;
-        for (int c : {1, 2, 3, 4, 6, 8}) {
-            if ((a.N + kOneSlots * c - 1) / (kOneSlots * c) <= kGemvTargetWgs) { ipw = c; break; }
-        }
+        const int ipw = one_ipw(a);
         const unsigned grid = (unsigned)((a.N + kOneSlots * ipw - 1) / (kOneSlots * ipw));
+        if (a.M > 4) {
+            switch (a.mode) {
+                case 0: return launch_one<0, 8>(a, ipw, grid, s);
+                case 1: return launch_one<1, 8>(a, ipw, grid, s);
+                default: return launch_one<2, 8>(a, ipw, grid, s);
+            }
+        }
+        if (a.M > 2) {
+            switch (a.mode) {
+                case 0: return launch_one<0, 4>(a, ipw, grid, s);
+                case 1: return launch_one<1, 4>(a, ipw, grid, s);
+                default: return launch_one<2, 4>(a, ipw, grid, s);
+            }
+        }
         if (a.M == 2) {
             switch (a.mode) {
                 case 0: return launch_one<0, 2>(a, ipw, grid, s);
