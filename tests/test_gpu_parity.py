@@ -172,6 +172,8 @@ GEMV_CASES = [
     (3, 2048, 20000, 128, None, 2),  # gate/up pairs
     (6, 1024, 16384, 128, None, 1),  # 8 groups per row, += residual
     (4, 4096, 16384, 128, None, 0),  # K split in 2
+    (7, 2048, 16384, 128, None, 2),  # tokens 0..6 of the two-token lane map
+    (4, 2048, 16500, 128, None, 1),
     # the limits the host checks: 8 tokens x K = 16384 (8 passes) on the dot4
     # kernel, the MFMA GEMV at its K = 8192, and K = 16384 in the
     # reference-native format

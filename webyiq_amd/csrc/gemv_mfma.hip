@@ -296,10 +296,12 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(MfmaGemvParams p) {
 // each group's two MFMAs and its fold step then run as soon as that group
 // lands (folding after the last group's MFMAs was 1-1.5 us slower on the
 // lm_head shapes).  Measured against 2 and 8 waves per workgroup, 4 is
-// fastest.  Splitting the fold between the wave's halves (MFMA rows 8..15
-// repeating tokens 0..7, odd pairs in the upper lanes, a lane exchange
-// before the tree) was measured much slower (38.9 -> 63.3 us at 8 tokens x
-// 151,936 rows) and is not used.
+// fastest.  The MFMA's token rows 8..15 are padding; the results of tokens
+// 4 q + 2, 4 q + 3 move into those lanes (two lane swaps per group), so
+// each lane folds two tokens, not four.  An earlier split of the fold
+// between the wave's halves (MFMA rows 8..15 repeating tokens 0..7, odd
+// pairs in the upper lanes, a lane exchange before the tree) was measured
+// much slower (38.9 -> 63.3 us at 8 tokens x 151,936 rows).
 // Store and argmax instances are held to 96 VGPRs: five workgroups per CU
 // (the LDS allows five) overlap one another's loads and compute (38.65
 // against 39.86 us at 8 tokens x 151,936 rows; six spill).
@@ -312,6 +314,7 @@ template <int MT, int MODE, bool ARGMAX>
 __global__ __launch_bounds__(64 * kRowsWaves, (MODE == 0 ? 5 : 1)) void gemv_mfma_rows_kernel(
     const uint32_t* kwq, const uint32_t* kws, const int8_t* kxq, const int32_t* kxs, const float* kdx, int kN, int kK,
     uint32_t kmg, MfmaGemvParams pk) {
+    static_assert(MT == 8, "the fold's lane map spreads tokens 0..7 over both halves of the wave");
     constexpr int NH = MODE == 2 ? 2 : 1;
     constexpr int RB = 16 * kRowsWaves;  // rows per workgroup: one 16-row block per wave
     constexpr int NT = 64 * kRowsWaves;  // threads
@@ -346,7 +349,13 @@ __global__ __launch_bounds__(64 * kRowsWaves, (MODE == 0 ? 5 : 1)) void gemv_mfm
 
     const int m = c < MT ? c : MT - 1;  // token of this lane's activation operand
     const unsigned char* xr = xq_lds + m * K + 16 * 2 * q;
-    unsigned long long best[4] = {0, 0, 0, 0};  // keys of tokens 4 q + j (this lane's row)
+    // The MFMA result gives lane (q, c) tokens 4 q .. 4 q + 3 of row c; for
+    // q >= 2 those are padding rows (MT = 8).  Tokens 4 q + 2, 4 q + 3 of the
+    // lower half are swapped into the upper half (v_permlane32_swap: lane
+    // 32 + l takes lane l's value), so every lane folds two tokens: tp[j].
+    const int tp0 = lane < 32 ? 4 * q : 4 * q - 6;
+    const int tp[2] = {tp0, tp0 + 1};
+    unsigned long long best[2] = {0, 0};  // keys of tokens tp[j] (this lane's row)
 
     {
         const int64_t rr = (int64_t)blockIdx.x * RB + 16 * wave + c;  // this lane's row
@@ -397,11 +406,11 @@ __global__ __launch_bounds__(64 * kRowsWaves, (MODE == 0 ? 5 : 1)) void gemv_mfm
         // pair of groups (those that exist); the pairwise tree over the 8
         // pairs follows
         const int rows_total = NH * (int)N;
-        float cc[NH][4][8];
+        float cc[NH][2][8];
 #pragma unroll
         for (int h = 0; h < NH; ++h)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int k = 0; k < 8; ++k) cc[h][j][k] = 0.0f;
 #pragma unroll
@@ -418,10 +427,13 @@ __global__ __launch_bounds__(64 * kRowsWaves, (MODE == 0 ? 5 : 1)) void gemv_mfm
                 v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, v4i{0, 0, 0, 0}, 0, 0, 0);
                 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, d, 0, 0, 0);
                 const float2 w = sm_lds[(h * RB + 16 * wave + c) * NGP + i];
+                const auto s02 = __builtin_amdgcn_permlane32_swap((uint32_t)d[0], (uint32_t)d[2], false, false);
+                const auto s13 = __builtin_amdgcn_permlane32_swap((uint32_t)d[1], (uint32_t)d[3], false, false);
+                const int e[2] = {(int)s02[0], (int)s13[0]};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
-                    cc[h][j][i / 2] = fmaf(w.y, (float)xs_lds[t * NG + i], fmaf(w.x, (float)d[j], cc[h][j][i / 2]));
+                for (int j = 0; j < 2; ++j) {
+                    const int t = tp[j] < MT ? tp[j] : MT - 1;
+                    cc[h][j][i / 2] = fmaf(w.y, (float)xs_lds[t * NG + i], fmaf(w.x, (float)e[j], cc[h][j][i / 2]));
                 }
                 if (a.acc_dump) {  // test hook: the group sums the chains fold
 #pragma unroll
@@ -432,17 +444,17 @@ __global__ __launch_bounds__(64 * kRowsWaves, (MODE == 0 ? 5 : 1)) void gemv_mfm
                 }
             }
         }
-        float v[NH][4];
+        float v[NH][2];
 #pragma unroll
         for (int h = 0; h < NH; ++h)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int t = 4 * q + j < MT ? 4 * q + j : MT - 1;
+            for (int j = 0; j < 2; ++j) {
+                const int t = tp[j] < MT ? tp[j] : MT - 1;
                 v[h][j] = tree8(cc[h][j]) * dx_lds[t];
             }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int t = 4 * q + j;
+        for (int j = 0; j < 2; ++j) {
+            const int t = tp[j];
             if (t >= a.M || rr >= N) continue;
             if (ARGMAX) {
                 if (a.y) a.y[(int64_t)t * N + rr] = v[0][j];
@@ -467,14 +479,14 @@ __global__ __launch_bounds__(64 * kRowsWaves, (MODE == 0 ? 5 : 1)) void gemv_mfm
     // the workgroup's best key per token: over the wave's 16 rows by
     // shuffles, over the 4 waves through LDS; then the cross-workgroup combine
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
         unsigned long long key = best[j];
 #pragma unroll
         for (int o = 8; o > 0; o >>= 1) {
             const unsigned long long u = __shfl_xor(key, o, 16);
             key = u > key ? u : key;
         }
-        if (c == 0 && 4 * q + j < MT) wbest[wave * MT + 4 * q + j] = key;
+        if (c == 0 && tp[j] < MT) wbest[wave * MT + tp[j]] = key;
     }
     __syncthreads();
     unsigned long long wb = 0;
