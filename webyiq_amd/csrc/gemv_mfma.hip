@@ -406,6 +406,10 @@ __global__ __launch_bounds__(64 * kRowsWaves, (MODE == 0 ? 5 : 1)) void gemv_mfm
         // pair of groups (those that exist); the pairwise tree over the 8
         // pairs follows
         const int rows_total = NH * (int)N;
+        // this lane's two tokens' activation group sums
+        const int32_t* xsp[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) xsp[j] = xs_lds + (tp[j] < MT ? tp[j] : MT - 1) * NG;
         float cc[NH][2][8];
 #pragma unroll
         for (int h = 0; h < NH; ++h)
@@ -426,15 +430,6 @@ __global__ __launch_bounds__(64 * kRowsWaves, (MODE == 0 ? 5 : 1)) void gemv_mfm
                              (int)(wv[h][i].w & kNibbleMask), (int)((wv[h][i].w >> 4) & kNibbleMask)};
                 v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, v4i{0, 0, 0, 0}, 0, 0, 0);
                 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, d, 0, 0, 0);
-                const float2 w = sm_lds[(h * RB + 16 * wave + c) * NGP + i];
-                const auto s02 = __builtin_amdgcn_permlane32_swap((uint32_t)d[0], (uint32_t)d[2], false, false);
-                const auto s13 = __builtin_amdgcn_permlane32_swap((uint32_t)d[1], (uint32_t)d[3], false, false);
-                const int e[2] = {(int)s02[0], (int)s13[0]};
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int t = tp[j] < MT ? tp[j] : MT - 1;
-                    cc[h][j][i / 2] = fmaf(w.y, (float)xs_lds[t * NG + i], fmaf(w.x, (float)e[j], cc[h][j][i / 2]));
-                }
                 if (a.acc_dump) {  // test hook: the group sums the chains fold
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
@@ -442,6 +437,13 @@ __global__ __launch_bounds__(64 * kRowsWaves, (MODE == 0 ? 5 : 1)) void gemv_mfm
                         if (t < a.M && rr < N) a.acc_dump[((int64_t)t * rows_total + h * N + rr) * NG + i] = d[j];
                     }
                 }
+                const float2 w = sm_lds[(h * RB + 16 * wave + c) * NGP + i];
+                const auto s02 = __builtin_amdgcn_permlane32_swap((uint32_t)d[0], (uint32_t)d[2], false, false);
+                const auto s13 = __builtin_amdgcn_permlane32_swap((uint32_t)d[1], (uint32_t)d[3], false, false);
+                const int e[2] = {(int)s02[0], (int)s13[0]};
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    cc[h][j][i / 2] = fmaf(w.y, (float)xsp[j][i], fmaf(w.x, (float)e[j], cc[h][j][i / 2]));
             }
         }
         float v[NH][2];
