@@ -187,9 +187,17 @@ class TimingEvents:
                 self.hip.hipEventDestroy(e)
 
 
-def graph_time(torch, launches, reps):
+def settle_reps(launches, n=512):
+    """Replays of a graph of `launches` that make about n launches: enough
+    back-to-back load for the clocks to settle before a timing."""
+    return max(2, -(-n // len(launches)))
+
+
+def graph_time(torch, launches, reps, warm=0):
     """Mean time per launch of `launches` captured in one HIP graph and
-    replayed `reps` times back to back (seconds)."""
+    replayed `reps` times back to back (seconds).  `warm` untimed replays are
+    queued right before the timed ones, with no synchronisation between, so
+    the timing starts on a busy GPU at settled clocks."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -207,6 +215,8 @@ def graph_time(torch, launches, reps):
     ev = TimingEvents(torch)
     torch.cuda.synchronize()
     cur = torch.cuda.current_stream()
+    for _ in range(warm):
+        g.replay()
     ev.record(0, cur)
     for _ in range(reps):
         g.replay()
@@ -653,8 +663,7 @@ def bench_configs(torch, lib, ops, orc):
             want = orc.linear(to_host_u32(ws[0][0]), to_host_u32(ws[0][1]), K, G, *host_acts(a))
             gates[f"cfg3_M{M}_{name}"] = parity_gate(
                 f"cfg 3 M={M} {name}", np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32)))
-            graph_time(torch, launches, 2)
-            t = graph_time(torch, launches, max(2, 256 // R))
+            t = graph_time(torch, launches, max(2, 256 // R), warm=settle_reps(launches))
             verify[f"M{M}_{name}_K{K}_N{N}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1)}
             del ws
     res["cfg3_verify_gemv"] = verify
@@ -697,8 +706,7 @@ def bench_configs(torch, lib, ops, orc):
     gates["cfg2_block"] = parity_gate(
         "cfg 2 block", rel_h < 1e-5 and np.array_equal(host_acts(a2)[0], q2)
         and np.array_equal(yres.cpu().numpy().view(np.uint32), y_want.view(np.uint32)), f"(gate_up rel {rel_h:.3g})")
-    graph_time(torch, fused, 2)
-    t2 = graph_time(torch, fused, max(2, 128 // R)) * 2  # per block (2 launches)
+    t2 = graph_time(torch, fused, max(2, 128 // R), warm=settle_reps(fused)) * 2  # per block (2 launches)
     steps = []
     for (qg, sg), (qd, sd) in zip(gu, dn):
         steps.append(Launcher(lib, "wq_quant_act", [P(x.data_ptr()), P(nw.data_ptr()), ctypes.c_float(1e-6), 1, K1,
@@ -709,8 +717,7 @@ def bench_configs(torch, lib, ops, orc):
                                                     P(a2.xq.data_ptr()), P(a2.dx.data_ptr()), P(a2.xs.data_ptr())]))
         steps.append(Launcher(lib, "wq_gemv", [P(qd.data_ptr()), P(sd.data_ptr()), K1, F, G, P(a2.xq.data_ptr()),
                                                P(a2.dx.data_ptr()), P(a2.xs.data_ptr()), 1, F, 1, P(yres.data_ptr())]))
-    graph_time(torch, steps, 2)
-    t4 = graph_time(torch, steps, max(2, 128 // R)) * 4  # per block (4 launches)
+    t4 = graph_time(torch, steps, max(2, 128 // R), warm=settle_reps(steps)) * 4  # per block (4 launches)
     nb_block = nb_gu + nb_q + nb_dn
     res["cfg2_decode_mlp_block"] = {"us": round(t2 * 1e6, 3), "bytes": nb_block,
                                     "GBps": round(nb_block / t2 / 1e9, 1), "launches": 2,
@@ -735,8 +742,7 @@ def bench_configs(torch, lib, ops, orc):
             logits = oracle_rows(orc, to_host_u32(ws[0][0]), to_host_u32(ws[0][1]), 2048, G, *host_acts(a))
             gates[f"cfg5_M{M}_V{V}"] = parity_gate(
                 f"cfg 5 M={M} V={V}", np.array_equal(tok.cpu().numpy().view(np.uint32), orc.argmax(logits)))
-            graph_time(torch, launches, 2)
-            t = graph_time(torch, launches, max(2, 64 // R))
+            t = graph_time(torch, launches, max(2, 64 // R), warm=settle_reps(launches))
             nb = nbw + M * 2048 + 4 * M + 4 * M * 2048 // G + 4 * M
             head[f"M{M}_V{V}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1),
                                   "frac_hbm": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)}
@@ -757,8 +763,7 @@ def bench_configs(torch, lib, ops, orc):
         launches = [Launcher(lib, "wq_gemv", [P(q.data_ptr()), P(sc.data_ptr()), N, K, G, P(a.xq.data_ptr()),
                                               P(a.dx.data_ptr()), P(a.xs.data_ptr()), 1, K, 0, P(y.data_ptr())])
                     for q, sc in ws]
-        graph_time(torch, launches, 2)
-        t = graph_time(torch, launches, max(2, 256 // R))
+        t = graph_time(torch, launches, max(2, 256 // R), warm=settle_reps(launches))
         shard[f"cfg1_P{Pn}_N{N}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1)}
         del ws
     Vs = 151936 // 8
@@ -773,8 +778,7 @@ def bench_configs(torch, lib, ops, orc):
                                                         P(a.xq.data_ptr()), P(a.dx.data_ptr()), P(a.xs.data_ptr()),
                                                         M, 2048, P(ids.data_ptr()), None, P(tok.data_ptr()),
                                                         P(wsp.data_ptr()), wsp.numel()]) for q, sc in ws]
-        graph_time(torch, launches, 2)
-        t = graph_time(torch, launches, max(2, 128 // R))
+        t = graph_time(torch, launches, max(2, 128 // R), warm=settle_reps(launches))
         nb = nbw + M * 2048 + 4 * M + 4 * M * 2048 // G + 4 * M
         shard[f"cfg5_P8_M{M}_V{Vs}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1)}
     del ws
@@ -796,8 +800,7 @@ def bench_configs(torch, lib, ops, orc):
                                                      P(qd.data_ptr()), P(sd.data_ptr()), K1, Fs, G, 1, 1,
                                                      P(a2.xq.data_ptr()), P(a2.dx.data_ptr()), P(a2.xs.data_ptr()),
                                                      P(yres.data_ptr())]))
-    graph_time(torch, fused, 2)
-    t = graph_time(torch, fused, max(2, 128 // R)) * 2
+    t = graph_time(torch, fused, max(2, 128 // R), warm=settle_reps(fused)) * 2
     nb = nb_gu + 4 * Fs + Fs + 4 + 4 * (Fs // G) + nb_dn
     shard[f"cfg2_P8_gate_up_N{2 * Fs}_down_K{Fs}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1),
                                                      "launches": 2}
@@ -816,8 +819,7 @@ def bench_configs(torch, lib, ops, orc):
         launches = [Launcher(lib, "wq_gemv", [P(q.data_ptr()), P(sc.data_ptr()), N, K, 32, P(a.xq.data_ptr()),
                                               P(a.dx.data_ptr()), P(a.xs.data_ptr()), M, K, 0, P(y.data_ptr())])
                     for q, sc in ws]
-        graph_time(torch, launches, 2)
-        t = graph_time(torch, launches, max(2, 256 // R))
+        t = graph_time(torch, launches, max(2, 256 // R), warm=settle_reps(launches))
         g32[f"gemv_M{M}_K{K}_N{N}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1)}
         del ws
     M, K, N = 1024, 2048, 6144
@@ -847,8 +849,7 @@ def bench_configs(torch, lib, ops, orc):
         a = ops.empty_acts(M, 2 * Kh, 32, 32)
         ln = Launcher(lib, "wq_mtp_in", [P(emb.data_ptr()), P(xh.data_ptr())] + [P(t.data_ptr()) for t in nws] +
                       [ctypes.c_float(1e-6), M, Kh, P(a.xq.data_ptr()), P(a.dx.data_ptr()), P(a.xs.data_ptr())])
-        graph_time(torch, [ln] * 32, 2)
-        t = graph_time(torch, [ln] * 32, 8)
+        t = graph_time(torch, [ln] * 32, 8, warm=settle_reps([ln] * 32))
         nb = 4 * (2 * M * Kh + 3 * Kh) + 2 * M * Kh + 8 * (2 * M * Kh // 32)
         prod[f"mtp_in_M{M}_K{Kh}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1)}
     Hh, Dh, nch = 16, 128, 128
@@ -863,8 +864,7 @@ def bench_configs(torch, lib, ops, orc):
                                                  P(a.xq.data_ptr()), P(a.dx.data_ptr()), P(a.xs.data_ptr()),
                                                  None])
                for pt in parts]
-        graph_time(torch, lns, 2)
-        t = graph_time(torch, lns, 16)
+        t = graph_time(torch, lns, 16, warm=settle_reps(lns))
         nread = sum(Hh * ((pos + m + 32) // 32) * (Dh + 2) * 4 for m in range(M))
         nb = nread + M * Hh * Dh + 8 * (M * Hh * Dh // 32)
         prod[f"attn_combine_M{M}_pos{pos}"] = {"us": round(t * 1e6, 3), "GBps": round(nb / t / 1e9, 1)}
@@ -920,8 +920,8 @@ def bench_configs(torch, lib, ops, orc):
                 x.copy_(x0)
                 for lay in layers:
                     lay.run()
-        graph_time(torch, [Step()], 2)
-        t = graph_time(torch, [Step()], 10)
+        # one replay is 100-160 launches: five replays settle the clocks
+        t = graph_time(torch, [Step()], 10, warm=5)
         nbw = sum(lay.weight_bytes() for lay in layers)
         key = f"M{M}" + ("" if attention == "combine" else "_copy_attn") + ("" if fuse else "_unfused")
         # qkv, gate_up, down: quantiser + GEMV, one launch when fused and M <= 2;
