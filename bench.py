@@ -81,6 +81,9 @@ def parse():
     ap.add_argument("--settle", type=int, default=1000,
                     help="untimed GEMV launches (other weight copies), replayed as a graph ahead of "
                          "the warm-up: the gate that covers the host's enqueue and settles the clocks")
+    ap.add_argument("--config-settle", type=int, default=512,
+                    help="launches of the same graph queued right before each config timing "
+                         "(0: none; keeps the dispatches in flight few, e.g. under rocprofv3 --pmc)")
     ap.add_argument("--torch-events", action="store_true",
                     help="time with torch's default events (a system-scope fence at each record) "
                          "instead of HIP events created with hipEventDisableSystemFence")
@@ -187,10 +190,15 @@ class TimingEvents:
                 self.hip.hipEventDestroy(e)
 
 
-def settle_reps(launches, n=512):
-    """Replays of a graph of `launches` that make about n launches: enough
-    back-to-back load for the clocks to settle before a timing."""
-    return max(2, -(-n // len(launches)))
+CONFIG_SETTLE = 512  # launches queued before each config timing (--config-settle)
+
+
+def settle_reps(launches, n=None):
+    """Replays of a graph of `launches` that make about n launches
+    (default CONFIG_SETTLE): enough back-to-back load for the clocks to
+    settle before a timing.  n = 0 gives none."""
+    n = CONFIG_SETTLE if n is None else n
+    return 0 if n <= 0 else max(2, -(-n // len(launches)))
 
 
 def graph_time(torch, launches, reps, warm=0):
@@ -432,6 +440,8 @@ def main():
         out["prefill_detail"] = detail
 
     if not args.no_configs:
+        global CONFIG_SETTLE
+        CONFIG_SETTLE = max(0, args.config_settle)
         log("configs")
         out["configs"] = bench_configs(torch, lib, ops, orc)
 
@@ -921,7 +931,7 @@ def bench_configs(torch, lib, ops, orc):
                 for lay in layers:
                     lay.run()
         # one replay is 100-160 launches: five replays settle the clocks
-        t = graph_time(torch, [Step()], 10, warm=5)
+        t = graph_time(torch, [Step()], 10, warm=5 if CONFIG_SETTLE > 0 else 0)
         nbw = sum(lay.weight_bytes() for lay in layers)
         key = f"M{M}" + ("" if attention == "combine" else "_copy_attn") + ("" if fuse else "_unfused")
         # qkv, gate_up, down: quantiser + GEMV, one launch when fused and M <= 2;
